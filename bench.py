@@ -1,0 +1,371 @@
+"""Benchmark of the sparse shared-KV attention path on one MI355X.
+
+Workloads (synthetic, seeded; q / KV ~ N(0, 1) bf16, sinks ~ U(-1, 1), page 64,
+window 128, compression ratio 4, d_qk 576, d_v 512, scale 1/sqrt(576)):
+
+* ``decode128k`` (default, the figure ``value`` reports): B=128 sequences of
+  131072 tokens, 2 query tokens each (MTP), 128 heads, top-k 2048 compressed rows
+  per token drawn without replacement from the causally valid ones; block tables
+  a random permutation of a shared page pool.  HBM-bound.
+* ``prefill8k``: one sequence, 8192 query tokens over 8192 KV, 128 heads, top-k
+  2048 over the causally valid compressed rows (-1 padded).  MFMA-bound.
+* ``decode32``: B=32, 64 heads, KV lengths U[4096, 32768], top-k 512.
+
+A step is one forward call (row resolution, attention, split combine) with the
+split-KV plan built beforehand by the metadata op, replayed from a hipGraph.
+``value`` is microseconds per call (lower is better).  ``roofline`` rates the
+attention kernel alone, timed with HIP events on the stream it runs on.
+``cpu_baseline`` times the C oracle on a bounded sample of the same workload on
+the host cores and scales it to the full call.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+D_QK, D_V, PAGE, WIN, RATIO = 576, 512, 64, 128, 4
+ROW_BYTES = D_QK * 2
+FLOP_PER_ROW_HEAD = 2 * D_QK + 2 * D_V
+
+
+# ---------------------------------------------------------------------------
+# synthetic inputs, built on the GPU
+# ---------------------------------------------------------------------------
+def _random_subsets(n_tok, thr, K, space, gen, dev):
+    """Per token: min(K, thr) distinct ids from [0, thr) in random order, -1 padded."""
+    keys = torch.rand((n_tok, space), generator=gen, device=dev)
+    col = torch.arange(space, device=dev)[None, :]
+    keys = torch.where(col < thr[:, None], keys, torch.full_like(keys, 2.0))
+    order = torch.argsort(keys, dim=1)[:, :K].to(torch.int32)
+    take = torch.clamp(thr, max=K)
+    return torch.where(torch.arange(K, device=dev)[None, :] < take[:, None], order,
+                       torch.full_like(order, -1))
+
+
+def make_workload(name: str, seed: int = 0, dev="cuda"):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    if name == "decode128k":
+        B, q_per, H, ctx, K = 128, 2, 128, 131072, 2048
+        kv = [ctx] * B
+    elif name == "prefill8k":
+        B, q_per, H, K = 1, 8192, 128, 2048
+        kv = [8192]
+    elif name == "decode32":
+        B, q_per, H, K = 32, 1, 64, 512
+        rng = np.random.default_rng(seed)
+        kv = rng.integers(4096, 32769, size=B).tolist()
+    else:
+        raise ValueError(name)
+    T = B * q_per
+    pages = [math.ceil(x / PAGE) for x in kv]
+    cpages = [math.ceil((x // RATIO) / PAGE) for x in kv]
+    ori_pool = torch.randn((sum(pages), PAGE, 1, D_QK), dtype=torch.bfloat16, device=dev, generator=gen)
+    cmp_pool = torch.randn((sum(cpages), PAGE, 1, D_QK), dtype=torch.bfloat16, device=dev, generator=gen)
+    perm = torch.randperm(sum(pages), device=dev, generator=gen).to(torch.int32)
+    cperm = torch.randperm(sum(cpages), device=dev, generator=gen).to(torch.int32)
+    obt = torch.full((B, max(pages)), -1, dtype=torch.int32, device=dev)
+    cbt = torch.full((B, max(cpages)), -1, dtype=torch.int32, device=dev)
+    o = c = 0
+    for b in range(B):
+        obt[b, :pages[b]] = perm[o:o + pages[b]]
+        cbt[b, :cpages[b]] = cperm[c:c + cpages[b]]
+        o += pages[b]
+        c += cpages[b]
+    q = torch.randn((T, H, D_QK), dtype=torch.bfloat16, device=dev, generator=gen)
+    sinks = (torch.rand(H, device=dev, generator=gen) * 2 - 1).float()
+    cu = torch.arange(0, T + 1, q_per, dtype=torch.int32, device=dev)
+    seqused = torch.tensor(kv, dtype=torch.int32, device=dev)
+    b_of = torch.arange(T, device=dev) // q_per
+    s_loc = torch.arange(T, device=dev) % q_per
+    s_g = seqused[b_of] - q_per + s_loc
+    thr = torch.div(s_g + 1, RATIO, rounding_mode="floor")
+    space = int((max(kv) // RATIO))
+    idx = _random_subsets(T, thr, K, space, gen, dev).reshape(T, 1, K)
+    n_win = (s_g + 1 - torch.clamp(s_g - (WIN - 1), min=0)).clamp(min=0)
+    n_cmp = torch.clamp(thr, min=0, max=K)
+    # algorithmic work: unique KV rows per sequence, FLOPs per (row, head)
+    uniq = 0
+    ids = torch.where(idx.reshape(B, q_per * K) >= 0, idx.reshape(B, q_per * K),
+                      torch.full_like(idx.reshape(B, q_per * K), -1))
+    srt = torch.sort(ids, dim=1).values
+    distinct = ((srt[:, 1:] != srt[:, :-1]) & (srt[:, 1:] >= 0)).sum(1) + (srt[:, 0] >= 0).long()
+    win_lo = torch.clamp(s_g - (WIN - 1), min=0).reshape(B, q_per).min(1).values
+    win_hi = s_g.reshape(B, q_per).max(1).values
+    uniq = int(distinct.sum().item() + (win_hi - win_lo + 1).clamp(min=0).sum().item())
+    rows_total = int((n_win + n_cmp).sum().item())
+    alg_bytes = (T * H * D_QK * 2 + T * H * D_V * 2 + T * H * 4 + T * K * 4 + uniq * ROW_BYTES)
+    alg_flops = rows_total * H * FLOP_PER_ROW_HEAD
+    return dict(name=name, B=B, T=T, H=H, K=K, q_per=q_per, kv=kv, q=q, ori_kv=ori_pool,
+                cmp_kv=cmp_pool, ori_bt=obt, cmp_bt=cbt, idx=idx, sinks=sinks, cu=cu,
+                seqused=seqused, alg_bytes=alg_bytes, alg_flops=alg_flops, uniq_rows=uniq,
+                rows_total=rows_total)
+
+
+# ---------------------------------------------------------------------------
+# GPU timing
+# ---------------------------------------------------------------------------
+def _events_time(fn, n, stream):
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(n):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) * 1000.0 / n  # us per call
+
+
+def measure(wl, steps, warmup, core_num=256):
+    from dsv4_planb_amd import metadata as M
+    from dsv4_planb_amd import sparse_attn_sharedkv
+    from dsv4_planb_amd.api import build_launch
+    from dsv4_planb_amd.graph import SasGraph
+
+    dev = wl["q"].device
+    scale = 1.0 / math.sqrt(D_QK)
+    stream = torch.cuda.Stream(device=dev)  # all timed work runs on this stream
+    with torch.cuda.stream(stream):
+        t0 = time.perf_counter()
+        plan = M.sparse_attn_sharedkv_metadata(
+            num_heads_q=wl["H"], num_heads_kv=1, head_dim=D_QK, cu_seqlens_q=wl["cu"],
+            seqused_kv=wl["seqused"], batch_size=wl["B"], max_seqlen_q=wl["q_per"],
+            max_seqlen_kv=max(wl["kv"]), cmp_topk=wl["K"], cmp_ratio=RATIO, layout_q="TND",
+            has_cmp_kv=True, aic_core_num=core_num)
+        torch.cuda.synchronize()
+        plan_host_us = (time.perf_counter() - t0) * 1e6
+        cu = wl["cu"]
+        launch, out, lse = build_launch(
+            q_flat=wl["q"], ori_kv=wl["ori_kv"], ori_block_table=wl["ori_bt"], cmp_kv=wl["cmp_kv"],
+            cmp_block_table=wl["cmp_bt"], cmp_indices=wl["idx"], q_prefix=cu[:-1],
+            act_q_lens=cu[1:] - cu[:-1], seqused_kv=wl["seqused"], sinks=wl["sinks"],
+            metadata=plan, scenario=3, topk=wl["K"], cmp_ratio=RATIO, ori_win_left=WIN - 1,
+            softmax_scale=scale, core_num=core_num)
+        for _ in range(max(warmup, 1)):
+            launch.run()
+        torch.cuda.synchronize()
+        graph = SasGraph(launch)
+        for _ in range(max(warmup, 1)):
+            graph.replay(stream)
+        torch.cuda.synchronize()
+        # the timed region: `steps` full forward calls replayed from the graph
+        call_us = _events_time(lambda: graph.replay(stream), steps, stream)
+        torch.cuda.synchronize()
+        # the stages alone (same stream, same inputs)
+        attend_us = _events_time(lambda: launch.run("attend"), steps, stream)
+        resolve_us = _events_time(lambda: launch.run("resolve"), steps, stream)
+        combine_us = _events_time(lambda: launch.run("combine"), steps, stream)
+        plan_p = launch.params
+        from dsv4_planb_amd.metadata import device_plan
+        plan_us = _events_time(lambda: device_plan(plan_p, cu[:-1], cu[1:] - cu[:-1], wl["seqused"]),
+                               steps, stream)
+        # eager API call, host work included
+        api_kw = dict(ori_kv=wl["ori_kv"], cmp_kv=wl["cmp_kv"], cmp_sparse_indices=wl["idx"],
+                      ori_block_table=wl["ori_bt"], cmp_block_table=wl["cmp_bt"], cu_seqlens_q=cu,
+                      seqused_kv=wl["seqused"], sinks=wl["sinks"], metadata=plan,
+                      softmax_scale=scale, cmp_ratio=RATIO, topk_cmp=wl["K"])
+        sparse_attn_sharedkv(wl["q"], **api_kw)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            sparse_attn_sharedkv(wl["q"], **api_kw)
+        torch.cuda.synchronize()
+        eager_us = (time.perf_counter() - t1) * 1e6 / steps
+        graph.close()
+    ok = bool(torch.isfinite(out.float()).all().item())
+    return dict(call_us=call_us, attend_us=attend_us, resolve_us=resolve_us,
+                combine_us=combine_us, plan_us=plan_us, plan_host_us=plan_host_us,
+                eager_api_us=eager_us, finite=ok)
+
+
+def _traffic_from_profile(workload):
+    """HBM bytes per attention launch measured with rocprofv3 counters, if a
+    summary for this workload is committed (profiles/<kernel>_<workload>_pmc.json)."""
+    path = os.path.join(ROOT, "profiles", f"sas_fwd_{workload}_pmc.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            return float(json.load(f)["hbm_bytes_per_launch"])
+    except Exception:  # noqa: BLE001
+        return None
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the C oracle on a bounded sample of the same workload
+# ---------------------------------------------------------------------------
+def cpu_baseline(name, n_seq, seed=0):
+    from oracle import golden_c
+
+    wl_shape = dict(decode128k=(128, 2, 128, 131072, 2048), decode32=(32, 1, 64, 32768, 512),
+                    prefill8k=(1, 8192, 128, 8192, 2048))[name]
+    B_full, q_per, H, ctx, K = wl_shape
+    rng = np.random.default_rng(seed)
+    cores = len(os.sched_getaffinity(0))
+
+    def bf16_bits(n):
+        return (rng.standard_normal(n, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+    if name == "prefill8k":
+        # a stratified sample of query tokens of the one sequence
+        n_tok_full = q_per
+        tokens = np.linspace(0, q_per - 1, 256).astype(np.int64)
+        nb, T = 1, q_per
+        kv = [ctx]
+        q = np.zeros((T, H, D_QK), np.uint16)
+        q[tokens] = bf16_bits(len(tokens) * H * D_QK).reshape(len(tokens), H, D_QK)
+        ori = bf16_bits(ctx // PAGE * PAGE * D_QK).reshape(ctx // PAGE, PAGE, D_QK)
+        obt = np.arange(ctx // PAGE, dtype=np.int32)[None]
+        ncp = ctx // RATIO // PAGE
+        cmp = bf16_bits(ncp * PAGE * D_QK).reshape(ncp, PAGE, D_QK)
+        cbt = np.arange(ncp, dtype=np.int32)[None]
+        idx = np.full((T, K), -1, np.int32)
+        for t in tokens:
+            thr = (t + 1) // RATIO
+            idx[t, :min(thr, K)] = rng.permutation(thr)[:K]
+        sample = f"{len(tokens)} of {q_per} query tokens (stratified), scaled by token count"
+        cu = np.array([0, T], np.int32)
+        scale_up = n_tok_full / len(tokens)
+    else:
+        # Sequences share one window pool (3 pages) and one compressed pool: the
+        # oracle's cost depends on the shapes, not on which pages hold the rows.
+        nb = n_seq
+        kv = [ctx] * nb
+        T = nb * q_per
+        tokens = None
+        q = bf16_bits(T * H * D_QK).reshape(T, H, D_QK)
+        npg = math.ceil(ctx / PAGE)
+        obt = np.full((nb, npg), -1, np.int32)
+        obt[:, npg - 3:] = np.arange(3, dtype=np.int32)
+        ori = bf16_bits(3 * PAGE * D_QK).reshape(3, PAGE, D_QK)
+        ncp = math.ceil(ctx // RATIO / PAGE)
+        cmp = bf16_bits(ncp * PAGE * D_QK).reshape(ncp, PAGE, D_QK)
+        cbt = np.tile(np.arange(ncp, dtype=np.int32), (nb, 1))
+        idx = np.full((T, K), -1, np.int32)
+        for t in range(T):
+            thr = (ctx - q_per + t % q_per + 1) // RATIO
+            take = min(thr, K)
+            idx[t, :take] = rng.choice(thr, size=take, replace=False)
+        cu = np.arange(0, T + 1, q_per, dtype=np.int32)
+        sample = f"{nb} of {B_full} sequences ({T} query tokens), scaled by sequence count"
+        scale_up = B_full / nb
+    sinks = rng.uniform(-1, 1, H).astype(np.float32)
+    t0 = time.perf_counter()
+    golden_c.attention(q=q, ori_kv=ori, ori_block_table=obt, q_prefix=cu[:-1],
+                       act_q=np.diff(cu), seqused_kv=kv, sinks=sinks,
+                       softmax_scale=1.0 / math.sqrt(D_QK), scenario=3, cmp_kv=cmp,
+                       cmp_block_table=cbt, cmp_sparse_indices=idx, cmp_ratio=RATIO,
+                       d_v=D_V, q_dtype="bf16", kv_dtype="bf16", tokens=tokens, nthreads=cores)
+    secs = time.perf_counter() - t0
+    return dict(value=secs * 1e6 * scale_up, unit="us/call", cores=cores, kind="port",
+                sample=f"{sample}; sample took {secs:.2f} s")
+
+
+def main_r_batch(name):
+    return dict(decode128k=128, decode32=32, prefill8k=1)[name]
+
+
+# ---------------------------------------------------------------------------
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="decode128k",
+                    choices=["decode128k", "prefill8k", "decode32"])
+    ap.add_argument("--extra", default="prefill8k,decode32",
+                    help="comma-separated extra workloads reported under 'workloads' ('' = none)")
+    ap.add_argument("--cpu-seqs", type=int, default=0,
+                    help="cap on sampled sequences for the CPU baseline (0 = size for ~10 s)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the operator is a "
+                          "per-GPU kernel and sharding is data-parallel over sequences "
+                          "(no exchange); run with --gpus 1"}))
+        sys.exit(2)
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda:0")
+    results = {}
+    for name in [args.workload] + [w for w in args.extra.split(",") if w and w != args.workload]:
+        wl = make_workload(name, seed=0, dev=dev)
+        r = measure(wl, args.steps, args.warmup)
+        attend_s = r["attend_us"] * 1e-6
+        r.update(alg_bytes=wl["alg_bytes"], alg_flops=wl["alg_flops"], uniq_rows=wl["uniq_rows"],
+                 rows_total=wl["rows_total"],
+                 attend_gbs=wl["alg_bytes"] / attend_s / 1e9,
+                 attend_tflops=wl["alg_flops"] / attend_s / 1e12,
+                 call_gbs=wl["alg_bytes"] / (r["call_us"] * 1e-6) / 1e9,
+                 call_tflops=wl["alg_flops"] / (r["call_us"] * 1e-6) / 1e12)
+        results[name] = r
+        del wl
+        torch.cuda.empty_cache()
+
+    main_r = results[args.workload]
+    bound = "mfma" if args.workload == "prefill8k" else "hbm"
+    if bound == "hbm":
+        ach, peak, unit = main_r["attend_gbs"], HBM_PEAK_GBS, "GB/s"
+    else:
+        ach, peak, unit = main_r["attend_tflops"], MFMA_BF16_PEAK_TFLOPS, "TFLOP/s"
+    roofline = {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
+                "frac": round(ach / peak, 4), "traffic": _traffic_from_profile(args.workload),
+                "kernel": "sas::fwd_kernel", "kernel_us": round(main_r["attend_us"], 2),
+                "algorithmic_bytes": main_r["alg_bytes"], "algorithmic_flops": main_r["alg_flops"]}
+    cpu = None
+    if not args.no_cpu_baseline:
+        if args.workload == "prefill8k":
+            cpu = cpu_baseline(args.workload, 1)
+        else:  # size the sample for ~10 s of CPU work, from a one-sequence probe
+            probe = cpu_baseline(args.workload, 1)
+            per_seq_s = probe["value"] * 1e-6 / main_r_batch(args.workload)
+            n = int(max(1, min(main_r_batch(args.workload), 10.0 / max(per_seq_s, 1e-3))))
+            cpu = cpu_baseline(args.workload, n if args.cpu_seqs <= 0 else min(n, args.cpu_seqs))
+    desc = {
+        "decode128k": "decode: B=128 seqs x 131072 KV, 2 query tokens/seq, H=128, top-k 2048, "
+                      "window 128, ratio 4, page 64, d_qk 576 / d_v 512",
+        "prefill8k": "prefill: B=1, 8192 query tokens over 8192 KV, H=128, top-k 2048, "
+                     "window 128, ratio 4, page 64, d_qk 576 / d_v 512",
+        "decode32": "decode: B=32 seqs x U[4096,32768] KV, 1 query token, H=64, top-k 512, "
+                    "window 128, ratio 4, page 64, d_qk 576 / d_v 512",
+    }
+    line = {
+        "metric": "us/call of the sparse shared-KV attention forward (1x MI355X), with achieved "
+                  "HBM GB/s (decode) and MFMA TFLOP/s (prefill)",
+        "value": round(main_r["call_us"], 2),
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_r["call_us"] / 1000.0, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 q/KV, random page permutation, random top-k)",
+        "config": {"workload": desc[args.workload], "name": args.workload},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "workloads": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                      for k, v in results.items()},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

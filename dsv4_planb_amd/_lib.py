@@ -1,0 +1,128 @@
+"""ctypes binding of ``libsas_hip.so`` (the C ABI declared in ``include/sas.h``).
+
+The library is built in-tree (``dsv4_planb_amd/build.py``).  Loading fails
+loudly when it is missing: there is no CPU fallback for the operator.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsas_hip.so")
+
+SAS_OK = 0
+ERR_NAMES = {
+    -1: "SAS_ERR_NULL", -2: "SAS_ERR_SHAPE", -3: "SAS_ERR_DTYPE", -4: "SAS_ERR_SCENARIO",
+    -5: "SAS_ERR_MASK_MODE", -6: "SAS_ERR_HEADS", -7: "SAS_ERR_WORKSPACE", -8: "SAS_ERR_PLAN",
+    -9: "SAS_ERR_LAUNCH", -10: "SAS_ERR_METADATA", -11: "SAS_ERR_GRAPH",
+    -12: "SAS_ERR_NOT_IMPLEMENTED",
+}
+DT_BF16, DT_FP16, DT_FP8E4M3 = 1, 2, 3
+SAS_META_SIZE = 1024
+
+# Exported entry points (mirrors include/sas.h).
+SYMBOLS = (
+    "sas_strerror", "sas_version", "sas_validate", "sas_workspace_size", "sas_plan_size",
+    "sas_target_units", "sas_plan", "sas_forward", "sas_resolve", "sas_attend", "sas_combine",
+    "sas_debug_rows", "sas_graph_capture", "sas_graph_launch", "sas_graph_destroy",
+    "sas_metadata_legacy",
+)
+
+
+class SasParams(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32), ("total_tokens", ctypes.c_int32),
+        ("num_heads_q", ctypes.c_int32), ("num_heads_kv", ctypes.c_int32),
+        ("head_dim_qk", ctypes.c_int32), ("head_dim_v", ctypes.c_int32),
+        ("ori_block_num", ctypes.c_int32), ("ori_block_size", ctypes.c_int32),
+        ("ori_table_len", ctypes.c_int32),
+        ("cmp_block_num", ctypes.c_int32), ("cmp_block_size", ctypes.c_int32),
+        ("cmp_table_len", ctypes.c_int32),
+        ("ori_block_stride", ctypes.c_int64), ("ori_row_stride", ctypes.c_int64),
+        ("cmp_block_stride", ctypes.c_int64), ("cmp_row_stride", ctypes.c_int64),
+        ("topk", ctypes.c_int32), ("cmp_ratio", ctypes.c_int32), ("scenario", ctypes.c_int32),
+        ("ori_win_left", ctypes.c_int32), ("ori_win_right", ctypes.c_int32),
+        ("ori_mask_mode", ctypes.c_int32), ("cmp_mask_mode", ctypes.c_int32),
+        ("q_dtype", ctypes.c_int32), ("kv_dtype", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+        ("num_cus", ctypes.c_int32), ("units_per_cu", ctypes.c_int32),
+    ]
+
+
+class SasTensors(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "q", "ori_kv", "ori_block_table", "cmp_kv", "cmp_block_table", "cmp_sparse_indices",
+        "q_prefix", "act_q_lens", "seqused_kv", "sinks", "ori_kv_scale", "cmp_kv_scale",
+        "out", "lse")]
+
+
+class SasMetaArgs(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "num_heads_q", "num_heads_kv", "head_dim", "batch_size", "max_seqlen_q",
+        "max_seqlen_kv", "ori_topk", "cmp_topk", "cmp_ratio", "ori_mask_mode",
+        "cmp_mask_mode", "ori_win_left", "ori_win_right", "layout_q", "layout_kv",
+        "has_ori_kv", "has_cmp_kv", "aic_core_num", "aiv_core_num")]
+
+
+class SasError(RuntimeError):
+    def __init__(self, code: int, what: str = ""):
+        self.code = code
+        msg = f"{ERR_NAMES.get(code, code)}: {strerror(code)}"
+        super().__init__(f"{what}: {msg}" if what else msg)
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load():
+    """The loaded library; raises ``RuntimeError`` if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python dsv4_planb_amd/build.py` "
+                "(the sparse shared-KV operator has no CPU fallback)")
+        lib = ctypes.CDLL(LIB_PATH)
+        P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+        PP = ctypes.POINTER(SasParams)
+        PT = ctypes.POINTER(SasTensors)
+        lib.sas_strerror.argtypes, lib.sas_strerror.restype = [I], ctypes.c_char_p
+        lib.sas_version.argtypes, lib.sas_version.restype = [], I
+        lib.sas_validate.argtypes, lib.sas_validate.restype = [PP], I
+        lib.sas_workspace_size.argtypes = [PP, ctypes.POINTER(S)]
+        lib.sas_plan_size.argtypes = [PP, ctypes.POINTER(S)]
+        lib.sas_target_units.argtypes = [PP, ctypes.POINTER(ctypes.c_int32)]
+        lib.sas_plan.argtypes = [PP, P, P, P, P, S, P]
+        for fn in ("sas_forward", "sas_resolve", "sas_attend", "sas_combine"):
+            getattr(lib, fn).argtypes = [PP, PT, P, P, S, P]
+        lib.sas_debug_rows.argtypes = [PP, P, P, P, P]
+        lib.sas_graph_capture.argtypes = [PP, PT, P, P, S, P, ctypes.POINTER(P)]
+        lib.sas_graph_launch.argtypes = [P, P]
+        lib.sas_graph_destroy.argtypes = [P]
+        lib.sas_metadata_legacy.argtypes = [ctypes.POINTER(SasMetaArgs), P, ctypes.c_int32, P,
+                                            ctypes.c_int32, P, ctypes.c_int32, P, ctypes.c_int32, P]
+        for fn in SYMBOLS:
+            if fn != "sas_strerror":
+                getattr(lib, fn).restype = I
+        _lib = lib
+    return _lib
+
+
+def strerror(code: int) -> str:
+    try:
+        return load().sas_strerror(code).decode()
+    except Exception:  # noqa: BLE001 -- used while formatting another error
+        return "unknown"
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != SAS_OK:
+        raise SasError(rc, what)

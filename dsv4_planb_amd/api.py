@@ -1,0 +1,402 @@
+"""Host entry point of the MI355X sparse shared-KV attention operator.
+
+Drop-in for the reference's ``sparse_attn_sharedkv_tilelang/api.py``: same
+function name, keyword arguments, defaults, scenario resolution, layouts,
+return convention and exception types (``api.py:129-397``).  Underneath, the
+call goes through the C ABI of ``libsas_hip.so`` (``include/sas.h``) to gfx950
+HIP kernels; there is no CPU fallback.
+
+Differences from the reference, all extensions:
+
+* ``num_heads_q`` may be 1..128 (reference: 64), ``head_dim`` 512 or 576; with
+  576 the query/key width is 576 and the output is the first 512 (V) columns.
+* ``ori_win_left`` may be any value >= 0 (reference kernel: 127).
+* ``ori_kv`` / ``cmp_kv`` may be ``torch.float8_e4m3fn`` with per-row fp32
+  scales ``ori_kv_scale`` / ``cmp_kv_scale`` ``[block_num, block_size, 1]``.
+* paged KV may carry padded block / row strides (the reference benchmark's
+  stride-padded layout, ``sparse_attn_sharedkv_perf_compare.py:220-247``).
+* ``metadata`` may be the reference's int32[1024] table (accepted and
+  validated; the GPU builds its own split-KV plan for all CUs) or a plan from
+  :func:`dsv4_planb_amd.metadata.sparse_attn_sharedkv_metadata` with
+  ``aic_core_num > 36``.
+* No host synchronisation happens when every tensor is already on the device,
+  so the call can be captured into a graph.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _lib
+from ._lib import SasParams, SasTensors, SAS_META_SIZE
+
+DEFAULT_CORE_NUM = 256  # compute units of one MI355X (reference default: 24 Ascend cores)
+DEFAULT_BLOCK_I = 128  # the reference's KV tile width; kept for importers (api.py:44)
+
+_KERNEL_CACHE: dict = {}
+
+
+def _torch_to_sas_dtype(t: torch.dtype) -> int:
+    """Query / output dtype code (reference ``_torch_to_tilelang_dtype``, api.py:51-56)."""
+    if t == torch.bfloat16:
+        return _lib.DT_BF16
+    if t == torch.float16:
+        return _lib.DT_FP16
+    raise ValueError(f"unsupported torch dtype {t}")
+
+
+def _kv_dtype_code(kv: torch.Tensor, q_code: int) -> int:
+    if kv.dtype == torch.float8_e4m3fn:
+        return _lib.DT_FP8E4M3
+    code = _torch_to_sas_dtype(kv.dtype)
+    if code != q_code:
+        raise ValueError(f"kv dtype {kv.dtype} must match q dtype or be float8_e4m3fn")
+    return code
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _dev_i32(t: torch.Tensor, device) -> torch.Tensor:
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+def _paged_strides(kv: torch.Tensor, D: int, name: str):
+    if kv.dim() != 4:
+        raise ValueError(f"{name} must be paged [block_num, block_size, N2, D], got {tuple(kv.shape)}")
+    if kv.shape[3] != D:
+        raise ValueError(f"{name} head dim {kv.shape[3]} != q head dim {D}")
+    if kv.stride(3) != 1:
+        raise ValueError(f"{name} rows must be contiguous in the head dim")
+    return int(kv.stride(0)), int(kv.stride(1))
+
+
+def _stream_handle(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class SasLaunch:
+    """One fully described call: parameter block, tensor block, workspace."""
+
+    def __init__(self, params: SasParams, tensors: SasTensors, keep: list, plan, ws, device):
+        self.params = params
+        self.tensors = tensors
+        self._keep = keep  # tensors whose storage the raw pointers refer to
+        self.plan = plan
+        self.ws = ws
+        self.device = device
+
+    def run(self, stage: str = "forward"):
+        lib = _lib.load()
+        fn = getattr(lib, f"sas_{stage}")
+        rc = fn(ctypes.byref(self.params), ctypes.byref(self.tensors), _ptr(self.plan),
+                _ptr(self.ws), self.ws.numel(), _stream_handle(self.device))
+        _lib.check(rc, f"sas_{stage}")
+
+
+def build_launch(
+    *,
+    q_flat: torch.Tensor,
+    ori_kv: torch.Tensor,
+    ori_block_table: torch.Tensor,
+    cmp_kv: Optional[torch.Tensor],
+    cmp_block_table: Optional[torch.Tensor],
+    cmp_indices: Optional[torch.Tensor],
+    q_prefix: torch.Tensor,
+    act_q_lens: torch.Tensor,
+    seqused_kv: torch.Tensor,
+    sinks: torch.Tensor,
+    metadata: Optional[torch.Tensor],
+    scenario: int,
+    topk: int,
+    cmp_ratio: int,
+    ori_win_left: int,
+    softmax_scale: float,
+    core_num: int,
+    ori_kv_scale: Optional[torch.Tensor] = None,
+    cmp_kv_scale: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    lse: Optional[torch.Tensor] = None,
+    units_per_cu: int = 0,
+) -> Tuple[SasLaunch, torch.Tensor, torch.Tensor]:
+    """Validate, convert and lay out one call; returns (launch, out, lse)."""
+    lib = _lib.load()
+    dev = q_flat.device
+    if dev.type != "cuda":
+        raise ValueError("sparse_attn_sharedkv runs on the GPU: q must be a device tensor")
+    T, N1, D = q_flat.shape
+    q_code = _torch_to_sas_dtype(q_flat.dtype)
+    kv_code = _kv_dtype_code(ori_kv, q_code)
+    q_flat = q_flat.contiguous()
+    ori_kv = ori_kv.to(dev)
+    obs, ors = _paged_strides(ori_kv, D, "ori_kv")
+    p = SasParams()
+    p.batch = int(q_prefix.numel())
+    p.total_tokens = T
+    p.num_heads_q = N1
+    p.num_heads_kv = int(ori_kv.shape[2])
+    p.head_dim_qk = D
+    p.head_dim_v = 512
+    p.ori_block_num, p.ori_block_size = int(ori_kv.shape[0]), int(ori_kv.shape[1])
+    ori_bt = _dev_i32(ori_block_table, dev)
+    p.ori_table_len = int(ori_bt.shape[1])
+    p.ori_block_stride, p.ori_row_stride = obs, ors
+    keep = [q_flat, ori_kv, ori_bt]
+    cmp_bt = idx = None
+    if scenario >= 2:
+        cmp_kv = cmp_kv.to(dev)
+        if _kv_dtype_code(cmp_kv, q_code) != kv_code:
+            raise ValueError("ori_kv and cmp_kv must share a dtype")
+        cbs, crs = _paged_strides(cmp_kv, D, "cmp_kv")
+        cmp_bt = _dev_i32(cmp_block_table, dev)
+        p.cmp_block_num, p.cmp_block_size = int(cmp_kv.shape[0]), int(cmp_kv.shape[1])
+        p.cmp_table_len = int(cmp_bt.shape[1])
+        p.cmp_block_stride, p.cmp_row_stride = cbs, crs
+        keep += [cmp_kv, cmp_bt]
+    else:
+        cmp_kv = None
+        p.cmp_block_num = p.cmp_block_size = p.cmp_table_len = 1
+        p.cmp_block_stride = p.cmp_row_stride = D
+    if scenario == 3:
+        idx = _dev_i32(cmp_indices, dev).reshape(T, -1)
+        keep.append(idx)
+    p.topk = topk if scenario == 3 else 0
+    p.cmp_ratio = cmp_ratio
+    p.scenario = scenario
+    p.ori_win_left = ori_win_left
+    p.ori_win_right = 0
+    p.ori_mask_mode = 4
+    p.cmp_mask_mode = 3
+    p.q_dtype = q_code
+    p.kv_dtype = kv_code
+    p.softmax_scale = float(softmax_scale)
+    p.num_cus = int(core_num)
+    p.units_per_cu = int(units_per_cu)
+    rc = lib.sas_validate(ctypes.byref(p))
+    if rc == -6:  # heads: the reference raises ValueError for unsupported N1/N2 (api.py:279-282)
+        raise ValueError(f"num_heads_kv must be 1 and num_heads_q in [1, 128] "
+                         f"(got N1={N1}, N2={p.num_heads_kv}, D={D})")
+    if rc == -2 and D not in (512, 576):
+        raise ValueError(f"head_dim must be 512 or 576 (got {D})")
+    _lib.check(rc, "sparse_attn_sharedkv")
+
+    qp = _dev_i32(q_prefix, dev)
+    aq = _dev_i32(act_q_lens, dev)
+    skv = _dev_i32(seqused_kv, dev)
+    snk = sinks.to(device=dev, dtype=torch.float32).contiguous()
+    if snk.numel() != N1:
+        raise ValueError(f"sinks must have {N1} entries (got {snk.numel()})")
+    keep += [qp, aq, skv, snk]
+    osc = csc = None
+    if kv_code == _lib.DT_FP8E4M3:
+        if ori_kv_scale is None or (scenario >= 2 and cmp_kv_scale is None):
+            raise ValueError("float8 KV needs ori_kv_scale (and cmp_kv_scale)")
+        osc = ori_kv_scale.to(device=dev, dtype=torch.float32).contiguous()
+        keep.append(osc)
+        if scenario >= 2:
+            csc = cmp_kv_scale.to(device=dev, dtype=torch.float32).contiguous()
+            keep.append(csc)
+    if out is None:
+        out = torch.empty((T, N1, 512), dtype=q_flat.dtype, device=dev)
+    if lse is None:
+        lse = torch.empty((T, N1), dtype=torch.float32, device=dev)
+    keep += [out, lse]
+
+    plan = None
+    if metadata is not None:
+        n = metadata.numel()
+        if n != SAS_META_SIZE:  # anything but the reference table must be our plan
+            need = ctypes.c_size_t()
+            _lib.check(lib.sas_plan_size(ctypes.byref(p), ctypes.byref(need)), "sas_plan_size")
+            assert n == need.value, (
+                f"metadata must have {SAS_META_SIZE} int32 entries (reference table) or "
+                f"{need.value} (split-KV plan for these shapes); got {n}")
+            plan = metadata.to(device=dev, dtype=torch.int32).contiguous()
+            keep.append(plan)
+    ws_bytes = ctypes.c_size_t()
+    _lib.check(lib.sas_workspace_size(ctypes.byref(p), ctypes.byref(ws_bytes)), "sas_workspace_size")
+    ws = torch.empty(int(ws_bytes.value), dtype=torch.uint8, device=dev)
+    keep.append(ws)
+
+    t = SasTensors()
+    t.q, t.ori_kv, t.ori_block_table = q_flat.data_ptr(), ori_kv.data_ptr(), ori_bt.data_ptr()
+    t.cmp_kv = cmp_kv.data_ptr() if cmp_kv is not None else None
+    t.cmp_block_table = cmp_bt.data_ptr() if cmp_bt is not None else None
+    t.cmp_sparse_indices = idx.data_ptr() if idx is not None else None
+    t.q_prefix, t.act_q_lens, t.seqused_kv = qp.data_ptr(), aq.data_ptr(), skv.data_ptr()
+    t.sinks = snk.data_ptr()
+    t.ori_kv_scale = osc.data_ptr() if osc is not None else None
+    t.cmp_kv_scale = csc.data_ptr() if csc is not None else None
+    t.out, t.lse = out.data_ptr(), lse.data_ptr()
+    return SasLaunch(p, t, keep, plan, ws, dev), out, lse
+
+
+def _get_kernel(
+    *,
+    batch: int,
+    max_seq: int,
+    total_tokens: int,
+    ori_block_num: int,
+    ori_block_size: int,
+    ori_table_len: int,
+    cmp_block_num: int,
+    cmp_block_size: int,
+    cmp_table_len: int,
+    n_heads: int,
+    n_kv_heads: int,
+    head_dim: int,
+    topk_cmp: int,
+    cmp_ratio: int,
+    scenario: int,
+    ori_win_left: int,
+    softmax_scale: float,
+    dtype: str,
+    core_num: int,
+):
+    """The reference's compile-cache lookup (api.py:59-126).  HIP kernels are
+    compiled ahead of time, so this only validates and caches the static
+    parameters and returns ``func(11 tensors) -> (out, lse)`` with the
+    reference kernel's argument order (api.py:372-384)."""
+    key = (batch, max_seq, total_tokens, ori_block_num, ori_block_size, ori_table_len,
+           cmp_block_num, cmp_block_size, cmp_table_len, n_heads, n_kv_heads, head_dim,
+           topk_cmp, cmp_ratio, scenario, ori_win_left, round(softmax_scale, 8), dtype, core_num)
+    fn = _KERNEL_CACHE.get(key)
+    if fn is None:
+        if dtype not in ("bfloat16", "float16"):
+            raise ValueError(f"dtype must be bfloat16 or float16, got {dtype!r}")
+        assert scenario in (1, 2, 3), "scenario must be 1 (SWA), 2 (CFA) or 3 (SCFA)"
+        assert n_kv_heads == 1, "API constraint: n_kv_heads must be 1"
+        assert head_dim in (512, 576), "API constraint: head_dim must be 512 or 576"
+        assert topk_cmp >= 0
+        assert batch > 0 and total_tokens > 0
+        fn = _SasKernelFunc(scenario=scenario, topk=topk_cmp, cmp_ratio=cmp_ratio,
+                            ori_win_left=ori_win_left, softmax_scale=softmax_scale,
+                            core_num=core_num)
+        _KERNEL_CACHE[key] = fn
+    return fn
+
+
+class _SasKernelFunc:
+    """``func(Q, ori_KV, ori_block_table, cmp_KV, cmp_block_table, cmp_indices,
+    q_prefix, actual_q_len, actual_kv_len, Sinks, Metadata) -> (Output, LSE)``."""
+
+    def __init__(self, **static):
+        self.static = static
+
+    def __call__(self, Q, ori_KV, ori_block_table, cmp_KV, cmp_block_table, cmp_indices,
+                 q_prefix, actual_q_len, actual_kv_len, Sinks, Metadata):
+        s = self.static
+        launch, out, lse = build_launch(
+            q_flat=Q, ori_kv=ori_KV, ori_block_table=ori_block_table,
+            cmp_kv=cmp_KV if s["scenario"] >= 2 else None,
+            cmp_block_table=cmp_block_table if s["scenario"] >= 2 else None,
+            cmp_indices=cmp_indices if s["scenario"] == 3 else None,
+            q_prefix=q_prefix, act_q_lens=actual_q_len, seqused_kv=actual_kv_len, sinks=Sinks,
+            metadata=Metadata, scenario=s["scenario"], topk=s["topk"],
+            cmp_ratio=s["cmp_ratio"], ori_win_left=s["ori_win_left"],
+            softmax_scale=s["softmax_scale"], core_num=s["core_num"])
+        launch.run()
+        return out, lse
+
+
+def sparse_attn_sharedkv(
+    q: torch.Tensor,
+    *,
+    ori_kv: torch.Tensor,
+    cmp_kv: Optional[torch.Tensor] = None,
+    cmp_sparse_indices: Optional[torch.Tensor] = None,
+    ori_block_table: torch.Tensor,
+    cmp_block_table: Optional[torch.Tensor] = None,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    seqused_q: Optional[torch.Tensor] = None,
+    seqused_kv: torch.Tensor,
+    sinks: torch.Tensor,
+    metadata: Optional[torch.Tensor] = None,
+    softmax_scale: float,
+    cmp_ratio: Optional[int] = None,
+    ori_mask_mode: int = 4,
+    cmp_mask_mode: int = 3,
+    ori_win_left: int = 127,
+    ori_win_right: int = 0,
+    layout_q: str = "TND",
+    layout_kv: str = "PA_ND",
+    return_softmax_lse: bool = False,
+    core_num: int = DEFAULT_CORE_NUM,
+    topk_cmp: Optional[int] = None,
+    ori_kv_scale: Optional[torch.Tensor] = None,
+    cmp_kv_scale: Optional[torch.Tensor] = None,
+) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """Forward pass; returns ``attention_out`` in the layout of ``q`` (and the
+    fp32 LSE with the sink folded in when ``return_softmax_lse``).
+
+    Scenario by optional inputs (api.py:156-160, 196-202): no ``cmp_kv`` -> SWA
+    (1); ``cmp_kv`` without ``cmp_sparse_indices`` -> CFA (2); both -> SCFA (3).
+    ``seqused_q`` is accepted for API parity and unused, as in the reference.
+    """
+    del seqused_q
+    assert ori_mask_mode == 4, "only ori_mask_mode=4 supported"
+    assert cmp_mask_mode == 3 or cmp_kv is None, "only cmp_mask_mode=3 supported"
+    assert ori_win_right == 0, "only ori_win_right=0 supported"
+    assert layout_kv == "PA_ND", "only layout_kv=PA_ND supported"
+    assert layout_q in ("TND", "BSND"), f"unsupported layout_q={layout_q!r}"
+    _torch_to_sas_dtype(q.dtype)
+    dev = q.device
+
+    if cmp_kv is None:
+        scenario = 1
+    elif cmp_sparse_indices is None:
+        scenario = 2
+    else:
+        scenario = 3
+
+    if layout_q == "TND":
+        assert cu_seqlens_q is not None, "cu_seqlens_q is required for TND"
+        cu = _dev_i32(cu_seqlens_q, dev)
+        B = cu.numel() - 1
+        T = q.shape[0]
+        q_flat = q
+        q_prefix = cu[:-1]
+        act_q = cu[1:] - cu[:-1]
+        idx = cmp_sparse_indices if scenario == 3 else None
+    else:
+        B, S, N1, D = q.shape
+        T = B * S
+        q_flat = q.reshape(T, N1, D)
+        q_prefix = torch.arange(B, dtype=torch.int32, device=dev) * S
+        act_q = torch.full((B,), S, dtype=torch.int32, device=dev)
+        if cu_seqlens_q is not None:
+            cu = _dev_i32(cu_seqlens_q, dev)
+            act_q = cu[1:] - cu[:-1]
+        idx = None
+        if scenario == 3:
+            ci = cmp_sparse_indices
+            idx = ci.reshape(T, ci.shape[2], ci.shape[3])
+
+    K = 0
+    if scenario == 3:
+        N2 = idx.shape[1]
+        K = topk_cmp if topk_cmp is not None else idx.shape[2]
+        assert K == idx.shape[2], "topk_cmp does not match cmp_sparse_indices last dim"
+        if N2 != 1:
+            raise ValueError(f"only N2=1 supported (got N2={N2})")
+    cmp_ratio_eff = cmp_ratio if cmp_ratio is not None else 4
+
+    launch, out, lse = build_launch(
+        q_flat=q_flat, ori_kv=ori_kv, ori_block_table=ori_block_table,
+        cmp_kv=cmp_kv, cmp_block_table=cmp_block_table, cmp_indices=idx,
+        q_prefix=q_prefix, act_q_lens=act_q, seqused_kv=seqused_kv, sinks=sinks,
+        metadata=metadata, scenario=scenario, topk=K, cmp_ratio=cmp_ratio_eff,
+        ori_win_left=ori_win_left, softmax_scale=softmax_scale, core_num=core_num,
+        ori_kv_scale=ori_kv_scale, cmp_kv_scale=cmp_kv_scale)
+    launch.run()
+
+    if layout_q == "BSND":
+        out = out.reshape(B, S, out.shape[1], out.shape[2])
+        lse = lse.reshape(B, S, lse.shape[1])
+    if return_softmax_lse:
+        return out, lse
+    return out

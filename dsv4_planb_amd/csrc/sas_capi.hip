@@ -1,0 +1,373 @@
+// sas_capi.hip -- extern "C" entry points of libsas_hip.so (declared in include/sas.h).
+//
+// Host side of the drop-in boundary: argument validation mirroring the
+// reference's guards (api.py:187-191, 279-282; kernel.py:96-108) as status
+// codes, workspace / plan sizing, and the stream-ordered launches of the
+// planner, resolver, attention and combine kernels.  Nothing here allocates
+// device memory or synchronises the host.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+
+#include "sas_common.h"
+#include "sas_kernels.hip"
+
+namespace {
+
+int esize(int dt) { return dt == SAS_DT_FP8E4M3 ? 1 : 2; }
+
+int query_num_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return n;
+}
+
+int target_units(const sas_params_t* p) {
+  int cus = p->num_cus > 0 ? p->num_cus : query_num_cus();
+  if (cus <= 0) cus = 256;
+  int per = p->units_per_cu > 0 ? p->units_per_cu : 1;
+  return cus * per;
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+SasFwdArgs fwd_args(const sas_params_t* p, int target) {
+  SasFwdArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.T = p->total_tokens;
+  a.H = p->num_heads_q;
+  a.B = p->batch;
+  a.scenario = p->scenario;
+  a.K = p->scenario == 3 ? p->topk : 0;
+  a.cmp_ratio = p->cmp_ratio > 0 ? p->cmp_ratio : 1;
+  a.ori_block_size = p->ori_block_size;
+  a.ori_table_len = p->ori_table_len;
+  a.ori_block_num = p->ori_block_num;
+  a.cmp_block_size = p->scenario >= 2 ? p->cmp_block_size : 1;
+  a.cmp_table_len = p->scenario >= 2 ? p->cmp_table_len : 1;
+  a.cmp_block_num = p->scenario >= 2 ? p->cmp_block_num : 1;
+  a.ori_block_stride = p->ori_block_stride;
+  a.ori_row_stride = p->ori_row_stride;
+  a.cmp_block_stride = p->scenario >= 2 ? p->cmp_block_stride : 0;
+  a.cmp_row_stride = p->scenario >= 2 ? p->cmp_row_stride : 0;
+  a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
+  a.win_left = p->ori_win_left;
+  a.list_stride = (int)sas_row_list_stride(p->ori_win_left, a.K, p->scenario);
+  a.unit_cap = (int)sas_plan_layout(p->total_tokens, target).unit_cap;
+  a.split_cap = target;
+  return a;
+}
+
+SasPlanArgs plan_args(const sas_params_t* p, int target) {
+  SasPlanArgs a;
+  a.T = p->total_tokens;
+  a.B = p->batch;
+  a.scenario = p->scenario;
+  a.win_left = p->ori_win_left;
+  a.cmp_ratio = p->cmp_ratio > 0 ? p->cmp_ratio : 1;
+  a.K = p->scenario == 3 ? p->topk : 0;
+  a.H = p->num_heads_q;
+  a.target = target;
+  return a;
+}
+
+int check_tensors(const sas_params_t* p, const sas_tensors_t* t) {
+  if (!t) return SAS_ERR_NULL;
+  if (!t->q || !t->ori_kv || !t->ori_block_table || !t->q_prefix || !t->act_q_lens ||
+      !t->seqused_kv || !t->sinks || !t->out)
+    return SAS_ERR_NULL;
+  if (p->scenario >= 2 && (!t->cmp_kv || !t->cmp_block_table)) return SAS_ERR_SCENARIO;
+  if (p->scenario == 3 && !t->cmp_sparse_indices) return SAS_ERR_SCENARIO;
+  if (p->kv_dtype == SAS_DT_FP8E4M3 &&
+      (!t->ori_kv_scale || (p->scenario >= 2 && !t->cmp_kv_scale)))
+    return SAS_ERR_NULL;
+  if (!aligned16(t->q) || !aligned16(t->out) || !aligned16(t->ori_kv) ||
+      (t->cmp_kv && !aligned16(t->cmp_kv)))
+    return SAS_ERR_SHAPE;
+  return SAS_OK;
+}
+
+struct Ws {
+  int* rows;
+  int* ncmp;
+  int* plan;
+  float* o;
+  float* ml;
+};
+
+int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out) {
+  const SasWsLayout W = sas_ws_layout(p->total_tokens, p->scenario == 3 ? p->topk : 0,
+                                      p->num_heads_q, p->head_dim_v, target, p->scenario,
+                                      p->ori_win_left);
+  if (!ws || ws_bytes < W.total) return SAS_ERR_WORKSPACE;
+  if (((uintptr_t)ws & 255u) != 0) return SAS_ERR_WORKSPACE;
+  char* base = static_cast<char*>(ws);
+  out->rows = reinterpret_cast<int*>(base + W.off_rows);
+  out->ncmp = reinterpret_cast<int*>(base + W.off_ncmp);
+  out->plan = reinterpret_cast<int*>(base + W.off_plan);
+  out->o = reinterpret_cast<float*>(base + W.off_o);
+  out->ml = reinterpret_cast<float*>(base + W.off_ml);
+  return SAS_OK;
+}
+
+typedef void (*fwd_fn_t)(SasFwdArgs, const uint16_t*, const uint8_t*, const uint8_t*,
+                         const float*, const float*, const int*, const int*, const int*,
+                         const int*, const float*, const int*, uint16_t*, float*, float*, float*);
+
+template <int NW, int DQK, int QT, bool KV8>
+fwd_fn_t fwd_ptr() {
+  return &sas::fwd_kernel<NW, DQK, QT, KV8>;
+}
+
+template <int NW, int DQK>
+fwd_fn_t pick_dtype(int qt, bool kv8) {
+  if (qt == 0) return kv8 ? fwd_ptr<NW, DQK, 0, true>() : fwd_ptr<NW, DQK, 0, false>();
+  return kv8 ? fwd_ptr<NW, DQK, 1, true>() : fwd_ptr<NW, DQK, 1, false>();
+}
+
+template <int NW>
+fwd_fn_t pick_dqk(int dqk, int qt, bool kv8) {
+  return dqk == 576 ? pick_dtype<NW, 576>(qt, kv8) : pick_dtype<NW, 512>(qt, kv8);
+}
+
+fwd_fn_t pick_fwd(const sas_params_t* p) {
+  const int qt = p->q_dtype == SAS_DT_BF16 ? 0 : 1;
+  const bool kv8 = p->kv_dtype == SAS_DT_FP8E4M3;
+  const int nw = (p->num_heads_q + 31) / 32;
+  if (nw <= 1) return pick_dqk<1>(p->head_dim_qk, qt, kv8);
+  if (nw == 2) return pick_dqk<2>(p->head_dim_qk, qt, kv8);
+  return pick_dqk<4>(p->head_dim_qk, qt, kv8);
+}
+
+int launch_status() { return hipGetLastError() == hipSuccess ? SAS_OK : SAS_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+const char* sas_strerror(int code) {
+  switch (code) {
+    case SAS_OK: return "ok";
+    case SAS_ERR_NULL: return "a required pointer is NULL";
+    case SAS_ERR_SHAPE: return "inconsistent or unsupported shape, stride or alignment";
+    case SAS_ERR_DTYPE: return "unsupported dtype combination";
+    case SAS_ERR_SCENARIO: return "scenario must be 1 (SWA), 2 (CFA) or 3 (SCFA) with its inputs";
+    case SAS_ERR_MASK_MODE: return "only ori_mask_mode=4, cmp_mask_mode=3, ori_win_right=0 supported";
+    case SAS_ERR_HEADS: return "num_heads_kv must be 1 and num_heads_q in [1, 128]";
+    case SAS_ERR_WORKSPACE: return "workspace missing, misaligned or too small";
+    case SAS_ERR_PLAN: return "plan buffer too small";
+    case SAS_ERR_LAUNCH: return "HIP kernel launch failed";
+    case SAS_ERR_METADATA: return "invalid metadata arguments";
+    case SAS_ERR_GRAPH: return "hipGraph capture or instantiation failed";
+    case SAS_ERR_NOT_IMPLEMENTED: return "not implemented";
+    default: return "unknown error";
+  }
+}
+
+int sas_version(void) { return 1; }
+
+int sas_validate(const sas_params_t* p) {
+  if (!p) return SAS_ERR_NULL;
+  if (p->num_heads_kv != 1 || p->num_heads_q < 1 || p->num_heads_q > 128) return SAS_ERR_HEADS;
+  if (p->scenario < 1 || p->scenario > 3) return SAS_ERR_SCENARIO;
+  if (p->ori_mask_mode != 4 || p->ori_win_right != 0 || p->ori_win_left < 0) return SAS_ERR_MASK_MODE;
+  if (p->scenario >= 2 && p->cmp_mask_mode != 3) return SAS_ERR_MASK_MODE;
+  if (p->q_dtype != SAS_DT_BF16 && p->q_dtype != SAS_DT_FP16) return SAS_ERR_DTYPE;
+  if (p->kv_dtype != p->q_dtype && p->kv_dtype != SAS_DT_FP8E4M3) return SAS_ERR_DTYPE;
+  if (p->batch < 1 || p->total_tokens < 0) return SAS_ERR_SHAPE;
+  if (p->head_dim_qk != 512 && p->head_dim_qk != 576) return SAS_ERR_SHAPE;
+  if (p->head_dim_v != 512) return SAS_ERR_SHAPE;
+  if (!std::isfinite(p->softmax_scale)) return SAS_ERR_SHAPE;
+  if (p->num_cus < 0 || p->units_per_cu < 0) return SAS_ERR_SHAPE;
+  const int es = esize(p->kv_dtype);
+  if (p->ori_block_num < 1 || p->ori_block_size < 1 || p->ori_table_len < 1) return SAS_ERR_SHAPE;
+  if (p->ori_row_stride < p->head_dim_qk ||
+      p->ori_block_stride < (int64_t)p->ori_block_size * p->ori_row_stride)
+    return SAS_ERR_SHAPE;
+  if ((p->ori_row_stride * es) % 16 != 0 || (p->ori_block_stride * es) % 16 != 0) return SAS_ERR_SHAPE;
+  if (p->scenario >= 2) {
+    if (p->cmp_ratio < 1) return SAS_ERR_SCENARIO;
+    if (p->cmp_block_num < 1 || p->cmp_block_size < 1 || p->cmp_table_len < 1) return SAS_ERR_SHAPE;
+    if (p->cmp_row_stride < p->head_dim_qk ||
+        p->cmp_block_stride < (int64_t)p->cmp_block_size * p->cmp_row_stride)
+      return SAS_ERR_SHAPE;
+    if ((p->cmp_row_stride * es) % 16 != 0 || (p->cmp_block_stride * es) % 16 != 0)
+      return SAS_ERR_SHAPE;
+    if ((int64_t)p->cmp_block_num * p->cmp_block_size >= (int64_t)1 << 31) return SAS_ERR_SHAPE;
+  }
+  if (p->scenario == 3 && p->topk < 1) return SAS_ERR_SCENARIO;
+  if ((int64_t)p->total_tokens * (p->scenario == 3 ? p->topk : 1) >= (int64_t)1 << 31)
+    return SAS_ERR_SHAPE;
+  return SAS_OK;
+}
+
+int sas_target_units(const sas_params_t* p, int32_t* units) {
+  if (!p || !units) return SAS_ERR_NULL;
+  *units = target_units(p);
+  return SAS_OK;
+}
+
+int sas_plan_size(const sas_params_t* p, size_t* n) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if (!n) return SAS_ERR_NULL;
+  *n = (size_t)sas_plan_layout(p->total_tokens, target_units(p)).total;
+  return SAS_OK;
+}
+
+int sas_workspace_size(const sas_params_t* p, size_t* bytes) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if (!bytes) return SAS_ERR_NULL;
+  *bytes = sas_ws_layout(p->total_tokens, p->scenario == 3 ? p->topk : 0, p->num_heads_q,
+                         p->head_dim_v, target_units(p), p->scenario, p->ori_win_left)
+               .total;
+  return SAS_OK;
+}
+
+int sas_plan(const sas_params_t* p, const int32_t* q_prefix, const int32_t* act_q_lens,
+             const int32_t* seqused_kv, int32_t* plan, size_t plan_n, sas_stream_t stream) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if (!q_prefix || !act_q_lens || !seqused_kv || !plan) return SAS_ERR_NULL;
+  const int target = target_units(p);
+  if (plan_n < (size_t)sas_plan_layout(p->total_tokens, target).total) return SAS_ERR_PLAN;
+  hipLaunchKernelGGL(sas::plan_kernel, dim3(1), dim3(sas::PLAN_NT), 0, (hipStream_t)stream,
+                     plan_args(p, target), q_prefix, act_q_lens, seqused_kv, plan);
+  return launch_status();
+}
+
+int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
+                size_t ws_bytes, sas_stream_t stream) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if ((rc = check_tensors(p, t))) return rc;
+  const int target = target_units(p);
+  Ws w;
+  if ((rc = carve(p, ws, ws_bytes, target, &w))) return rc;
+  if (!plan) plan = w.plan;
+  if (p->total_tokens == 0) return SAS_OK;
+  hipLaunchKernelGGL(sas::resolve_kernel, dim3(p->total_tokens), dim3(64), 0, (hipStream_t)stream,
+                     fwd_args(p, target), plan, t->ori_block_table, t->cmp_sparse_indices,
+                     t->cmp_block_table, w.rows, w.ncmp);
+  return launch_status();
+}
+
+int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
+               size_t ws_bytes, sas_stream_t stream) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if ((rc = check_tensors(p, t))) return rc;
+  const int target = target_units(p);
+  Ws w;
+  if ((rc = carve(p, ws, ws_bytes, target, &w))) return rc;
+  if (!plan) plan = w.plan;
+  if (p->total_tokens == 0) return SAS_OK;
+  const SasFwdArgs a = fwd_args(p, target);
+  fwd_fn_t fn = pick_fwd(p);
+  hipLaunchKernelGGL(fn, dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream, a,
+                     static_cast<const uint16_t*>(t->q), static_cast<const uint8_t*>(t->ori_kv),
+                     static_cast<const uint8_t*>(t->cmp_kv), t->ori_kv_scale, t->cmp_kv_scale,
+                     t->ori_block_table, t->cmp_block_table, w.rows, w.ncmp, t->sinks, plan,
+                     static_cast<uint16_t*>(t->out), t->lse, w.o, w.ml);
+  return launch_status();
+}
+
+int sas_combine(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
+                size_t ws_bytes, sas_stream_t stream) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if ((rc = check_tensors(p, t))) return rc;
+  const int target = target_units(p);
+  Ws w;
+  if ((rc = carve(p, ws, ws_bytes, target, &w))) return rc;
+  if (!plan) plan = w.plan;
+  if (p->total_tokens == 0) return SAS_OK;
+  const SasFwdArgs a = fwd_args(p, target);
+  if (p->q_dtype == SAS_DT_BF16)
+    hipLaunchKernelGGL(sas::combine_kernel<0>, dim3(target), dim3(256), 0, (hipStream_t)stream, a,
+                       plan, w.o, w.ml, static_cast<uint16_t*>(t->out), t->lse);
+  else
+    hipLaunchKernelGGL(sas::combine_kernel<1>, dim3(target), dim3(256), 0, (hipStream_t)stream, a,
+                       plan, w.o, w.ml, static_cast<uint16_t*>(t->out), t->lse);
+  return launch_status();
+}
+
+int sas_forward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
+                size_t ws_bytes, sas_stream_t stream) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if ((rc = check_tensors(p, t))) return rc;
+  const int target = target_units(p);
+  Ws w;
+  if ((rc = carve(p, ws, ws_bytes, target, &w))) return rc;
+  if (p->total_tokens == 0) return SAS_OK;
+  if (!plan) {
+    hipLaunchKernelGGL(sas::plan_kernel, dim3(1), dim3(sas::PLAN_NT), 0, (hipStream_t)stream,
+                       plan_args(p, target), t->q_prefix, t->act_q_lens, t->seqused_kv, w.plan);
+    if ((rc = launch_status())) return rc;
+    plan = w.plan;
+  }
+  if ((rc = sas_resolve(p, t, plan, ws, ws_bytes, stream))) return rc;
+  if ((rc = sas_attend(p, t, plan, ws, ws_bytes, stream))) return rc;
+  return sas_combine(p, t, plan, ws, ws_bytes, stream);
+}
+
+int sas_debug_rows(const sas_params_t* p, const void* ws, int32_t* rows, int32_t* counts,
+                   sas_stream_t stream) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if (!ws || !rows || !counts) return SAS_ERR_NULL;
+  const int K = p->scenario == 3 ? p->topk : 0;
+  const SasWsLayout W = sas_ws_layout(p->total_tokens, K, p->num_heads_q, p->head_dim_v,
+                                      target_units(p), p->scenario, p->ori_win_left);
+  const size_t stride = (size_t)sas_row_list_stride(p->ori_win_left, K, p->scenario);
+  const char* base = static_cast<const char*>(ws);
+  if (hipMemcpyAsync(rows, base + W.off_rows, (size_t)p->total_tokens * stride * 4,
+                     hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)
+    return SAS_ERR_LAUNCH;
+  if (hipMemcpyAsync(counts, base + W.off_ncmp, (size_t)p->total_tokens * 4,
+                     hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)
+    return SAS_ERR_LAUNCH;
+  return SAS_OK;
+}
+
+int sas_graph_capture(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
+                      size_t ws_bytes, sas_stream_t stream, void** graph_exec) {
+  if (!graph_exec) return SAS_ERR_NULL;
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if ((rc = check_tensors(p, t))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  hipGraph_t graph = nullptr;
+  if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return SAS_ERR_GRAPH;
+  rc = sas_forward(p, t, plan, ws, ws_bytes, stream);
+  hipError_t e = hipStreamEndCapture(s, &graph);
+  if (rc) {
+    if (graph) hipGraphDestroy(graph);
+    return rc;
+  }
+  if (e != hipSuccess || !graph) return SAS_ERR_GRAPH;
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  hipGraphDestroy(graph);
+  if (e != hipSuccess) return SAS_ERR_GRAPH;
+  *graph_exec = exec;
+  return SAS_OK;
+}
+
+int sas_graph_launch(void* graph_exec, sas_stream_t stream) {
+  if (!graph_exec) return SAS_ERR_NULL;
+  return hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream) == hipSuccess
+             ? SAS_OK
+             : SAS_ERR_GRAPH;
+}
+
+int sas_graph_destroy(void* graph_exec) {
+  if (!graph_exec) return SAS_ERR_NULL;
+  return hipGraphExecDestroy((hipGraphExec_t)graph_exec) == hipSuccess ? SAS_OK : SAS_ERR_GRAPH;
+}
+
+}  // extern "C"

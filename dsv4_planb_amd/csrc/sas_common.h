@@ -1,0 +1,104 @@
+// sas_common.h -- shared definitions of the gfx950 sparse shared-KV attention
+// kernels and their host launchers (plan layout, workspace layout, params).
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/sas.h"
+
+#ifdef __HIPCC__
+#define SAS_HD __host__ __device__
+#else
+#define SAS_HD
+#endif
+
+// ---- split-KV plan (int32 buffer written by the planner kernel) ----
+// header
+#define SAS_PLAN_MAGIC 0x53415350  // 'SASP'
+#define SAS_PLAN_VERSION 1
+#define SAS_PLAN_HDR 16
+enum {
+  PH_MAGIC = 0, PH_VERSION, PH_T, PH_UNITS, PH_CHUNK, PH_TARGET, PH_NSPLIT_TOKENS,
+  PH_NSLOTS, PH_TOTAL_ROWS_LO, PH_TOTAL_ROWS_HI, PH_H, PH_UNIT_CAP, PH_SCENARIO, PH_K
+};
+// per-token record [T][8]
+#define SAS_TOK_W 8
+enum { TK_B = 0, TK_S, TK_SG, TK_NWIN, TK_WINLO, TK_NCMPMAX, TK_SPLITS, TK_WSBASE };
+// per-unit record [unit_cap][4]: token, first row, end row, split index (-1 = padded token)
+#define SAS_UNIT_W 4
+
+// KV rows processed per inner tile by the attention kernel.
+#define SAS_TILE 32
+#define SAS_MIN_CHUNK 64
+
+struct SasPlanLayout {
+  int64_t T, target, unit_cap, split_cap;
+  int64_t off_tok, off_units, off_split_tokens, total;  // int32 offsets
+};
+
+SAS_HD static inline SasPlanLayout sas_plan_layout(int64_t T, int64_t target) {
+  SasPlanLayout L;
+  L.T = T;
+  L.target = target;
+  L.unit_cap = T + target;
+  L.split_cap = target;
+  L.off_tok = SAS_PLAN_HDR;
+  L.off_units = L.off_tok + SAS_TOK_W * T;
+  L.off_split_tokens = L.off_units + SAS_UNIT_W * L.unit_cap;
+  L.total = L.off_split_tokens + L.split_cap;
+  // A plan is never SAS_META_SIZE (1024) entries long, so a caller-supplied table
+  // is told apart from the reference's int32[1024] metadata by its size alone.
+  if (L.total == SAS_META_SIZE) L.total += 1;
+  return L;
+}
+
+// ---- workspace (bytes, each region 256-B aligned) ----
+struct SasWsLayout {
+  size_t off_rows, off_ncmp, off_plan, off_o, off_ml, total;
+  int64_t slot_cap;
+};
+
+SAS_HD static inline size_t sas_align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Row-code list of one token: window rows (win_left + 1 slots) then, in scenario 3,
+// the resolved compressed rows (topk slots).
+SAS_HD static inline int64_t sas_row_list_stride(int64_t win_left, int64_t K, int scenario) {
+  return win_left + 1 + (scenario == 3 ? K : 0);
+}
+
+SAS_HD static inline SasWsLayout sas_ws_layout(int64_t T, int64_t K, int64_t H, int64_t Dv,
+                                        int64_t target, int scenario, int64_t win_left) {
+  SasWsLayout W;
+  size_t off = 0;
+  W.off_rows = off;
+  off = sas_align256(off + (size_t)(T > 0 ? T : 1) * sas_row_list_stride(win_left, K, scenario) * 4);
+  W.off_ncmp = off;
+  off = sas_align256(off + (size_t)(T > 0 ? T : 1) * 4);
+  W.off_plan = off;
+  off = sas_align256(off + (size_t)sas_plan_layout(T, target).total * 4);
+  // split tokens have more rows than the chunk (>= total / target), so fewer
+  // than `target` of them exist and their units number at most 2 * target.
+  W.slot_cap = 2 * target;
+  W.off_o = off;
+  off = sas_align256(off + (size_t)W.slot_cap * H * Dv * 4);
+  W.off_ml = off;
+  off = sas_align256(off + (size_t)W.slot_cap * H * 2 * 4);
+  W.total = off;
+  return W;
+}
+
+// ---- kernel parameter blocks (passed by value) ----
+struct SasPlanArgs {
+  int32_t T, B, scenario, win_left, cmp_ratio, K, H, target;
+};
+
+struct SasFwdArgs {
+  int32_t T, H, B;
+  int32_t scenario, K, cmp_ratio;
+  int32_t win_left, list_stride;  // row-code list: win_left + 1 window slots (+ K)
+  int32_t ori_block_size, ori_table_len, ori_block_num;
+  int32_t cmp_block_size, cmp_table_len, cmp_block_num;
+  int64_t ori_block_stride, ori_row_stride, cmp_block_stride, cmp_row_stride;  // elements
+  float scale_log2;  // softmax_scale * log2(e)
+  int32_t unit_cap, split_cap;
+};

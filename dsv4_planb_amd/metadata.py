@@ -1,0 +1,226 @@
+"""Scheduler op of the sparse shared-KV attention path.
+
+Mirror of the reference's ``sparse_attn_sharedkv_tilelang/metadata.py``: same
+function, keyword arguments, defaults and module constants.
+
+* ``aic_core_num <= 36`` (the reference range; its default is 24): the exact
+  int32[1024] FA/FD table of the reference scheduler (metadata.py:258-1086),
+  computed on the host by ``sas_metadata_legacy`` in ``libsas_hip.so``.
+* ``aic_core_num > 36`` (e.g. the 256 CUs of an MI355X): the split-KV work plan
+  the GPU kernels consume, computed on the device by ``sas_plan``.  Its length
+  depends on the token count and is never 1024, so
+  :func:`dsv4_planb_amd.api.sparse_attn_sharedkv` tells the two apart by size.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import SasMetaArgs, SasParams
+
+# ---- constants mirrored from the reference (metadata.py:38-68) ----
+AIC_CORE_NUM = 36
+AIV_CORE_NUM = 72
+SAS_META_SIZE = 1024
+FA_METADATA_SIZE = 8
+FD_METADATA_SIZE = 8
+FA_CORE_ENABLE_INDEX = 0
+FA_BN2_START_INDEX = 1
+FA_M_START_INDEX = 2
+FA_S2_START_INDEX = 3
+FA_BN2_END_INDEX = 4
+FA_M_END_INDEX = 5
+FA_S2_END_INDEX = 6
+FA_FIRST_FD_DATA_WORKSPACE_IDX_INDEX = 7
+FD_CORE_ENABLE_INDEX = 0
+FD_BN2_IDX_INDEX = 1
+FD_M_IDX_INDEX = 2
+FD_WORKSPACE_IDX_INDEX = 3
+FD_WORKSPACE_NUM_INDEX = 4
+FD_M_START_INDEX = 5
+FD_M_NUM_INDEX = 6
+
+# split-KV plan header (csrc/sas_common.h)
+PLAN_MAGIC = 0x53415350
+PLAN_HDR = 16
+PLAN_TOK_W = 8
+PLAN_UNIT_W = 4
+
+_LAYOUT_Q = {"BSND": 0, "TND": 1, "BSH": 2}
+_LAYOUT_KV = {"PA_ND": 0, "TND": 1}
+
+
+def _host_i32(t) -> Optional[torch.Tensor]:
+    """Host int32 copy; an empty or absent tensor counts as absent
+    (the reference's ``_as_int_list``, metadata.py:331-341)."""
+    if t is None:
+        return None
+    if isinstance(t, (list, tuple)):
+        t = torch.tensor([int(x) for x in t], dtype=torch.int64)
+    if t.numel() == 0:
+        return None
+    return t.detach().to("cpu", torch.int64).to(torch.int32).contiguous()
+
+
+def _ptr_n(t: Optional[torch.Tensor]):
+    if t is None:
+        return None, 0
+    return ctypes.c_void_p(t.data_ptr()), int(t.numel())
+
+
+def legacy_table(*, num_heads_q, num_heads_kv, head_dim, cu_seqlens_q=None,
+                 cu_seqlens_ori_kv=None, seqused_q=None, seqused_kv=None, batch_size=0,
+                 max_seqlen_q=0, max_seqlen_kv=0, ori_topk=0, cmp_topk=0, cmp_ratio=-1,
+                 ori_mask_mode=4, cmp_mask_mode=3, ori_win_left=127, ori_win_right=0,
+                 layout_q="BSND", layout_kv="PA_ND", has_ori_kv=True, has_cmp_kv=True,
+                 aic_core_num=24, aiv_core_num=48) -> torch.Tensor:
+    """The reference int32[1024] table (metadata.py:974-1009) on the host."""
+    lib = _lib.load()
+    a = SasMetaArgs()
+    a.num_heads_q, a.num_heads_kv, a.head_dim = num_heads_q, num_heads_kv, head_dim
+    a.batch_size, a.max_seqlen_q, a.max_seqlen_kv = batch_size, max_seqlen_q, max_seqlen_kv
+    a.ori_topk, a.cmp_topk, a.cmp_ratio = ori_topk, cmp_topk, cmp_ratio
+    a.ori_mask_mode, a.cmp_mask_mode = ori_mask_mode, cmp_mask_mode
+    a.ori_win_left, a.ori_win_right = ori_win_left, ori_win_right
+    a.layout_q = _LAYOUT_Q.get(layout_q, 3)
+    a.layout_kv = _LAYOUT_KV.get(layout_kv, 2)
+    a.has_ori_kv, a.has_cmp_kv = int(bool(has_ori_kv)), int(bool(has_cmp_kv))
+    a.aic_core_num, a.aiv_core_num = aic_core_num, aiv_core_num
+    cq, ckv, uq, ukv = (_host_i32(x) for x in (cu_seqlens_q, cu_seqlens_ori_kv, seqused_q, seqused_kv))
+    out = torch.zeros(SAS_META_SIZE, dtype=torch.int32)
+    p_cq, n_cq = _ptr_n(cq)
+    p_ckv, n_ckv = _ptr_n(ckv)
+    p_uq, n_uq = _ptr_n(uq)
+    p_ukv, n_ukv = _ptr_n(ukv)
+    rc = lib.sas_metadata_legacy(ctypes.byref(a), p_cq, n_cq, p_ckv, n_ckv, p_uq, n_uq, p_ukv,
+                                 n_ukv, ctypes.c_void_p(out.data_ptr()))
+    if rc != 0:
+        raise ValueError(f"invalid metadata arguments ({_lib.strerror(rc)})")
+    return out
+
+
+def plan_params(*, total_tokens, batch, num_heads_q, scenario, topk, cmp_ratio, ori_win_left,
+                core_num, units_per_cu=0, head_dim=576) -> SasParams:
+    """A parameter block carrying what the planner reads (token count, batch,
+    heads, scenario, top-k, ratio, window, CU count); the KV fields hold
+    minimal valid values."""
+    p = SasParams()
+    p.batch, p.total_tokens = batch, total_tokens
+    p.num_heads_q, p.num_heads_kv = num_heads_q, 1
+    p.head_dim_qk = head_dim if head_dim in (512, 576) else 576
+    p.head_dim_v = 512
+    p.ori_block_num = p.ori_block_size = p.ori_table_len = 1
+    p.cmp_block_num = p.cmp_block_size = p.cmp_table_len = 1
+    p.ori_block_stride = p.ori_row_stride = p.head_dim_qk
+    p.cmp_block_stride = p.cmp_row_stride = p.head_dim_qk
+    p.topk = topk if scenario == 3 else 0
+    p.cmp_ratio = max(cmp_ratio, 1)
+    p.scenario = scenario
+    p.ori_win_left, p.ori_win_right = ori_win_left, 0
+    p.ori_mask_mode, p.cmp_mask_mode = 4, 3
+    p.q_dtype = p.kv_dtype = _lib.DT_BF16
+    p.softmax_scale = 1.0
+    p.num_cus, p.units_per_cu = core_num, units_per_cu
+    return p
+
+
+def plan_size(p: SasParams) -> int:
+    n = ctypes.c_size_t()
+    _lib.check(_lib.load().sas_plan_size(ctypes.byref(p), ctypes.byref(n)), "sas_plan_size")
+    return int(n.value)
+
+
+def device_plan(p: SasParams, q_prefix: torch.Tensor, act_q: torch.Tensor,
+                seqused_kv: torch.Tensor) -> torch.Tensor:
+    """Run the GPU planner on the current stream (no host synchronisation)."""
+    dev = q_prefix.device
+    n = plan_size(p)
+    plan = torch.empty(n, dtype=torch.int32, device=dev)
+    qp = q_prefix.to(device=dev, dtype=torch.int32).contiguous()
+    aq = act_q.to(device=dev, dtype=torch.int32).contiguous()
+    skv = seqused_kv.to(device=dev, dtype=torch.int32).contiguous()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    rc = _lib.load().sas_plan(ctypes.byref(p), ctypes.c_void_p(qp.data_ptr()),
+                              ctypes.c_void_p(aq.data_ptr()), ctypes.c_void_p(skv.data_ptr()),
+                              ctypes.c_void_p(plan.data_ptr()), n, stream)
+    _lib.check(rc, "sas_plan")
+    return plan
+
+
+def sparse_attn_sharedkv_metadata(
+    *,
+    num_heads_q: int,
+    num_heads_kv: int,
+    head_dim: int,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    cu_seqlens_ori_kv: Optional[torch.Tensor] = None,
+    cu_seqlens_cmp_kv: Optional[torch.Tensor] = None,
+    seqused_q: Optional[torch.Tensor] = None,
+    seqused_kv: Optional[torch.Tensor] = None,
+    batch_size: int = 0,
+    max_seqlen_q: int = 0,
+    max_seqlen_kv: int = 0,
+    ori_topk: int = 0,
+    cmp_topk: int = 0,
+    cmp_ratio: int = -1,
+    ori_mask_mode: int = 4,
+    cmp_mask_mode: int = 3,
+    ori_win_left: int = 127,
+    ori_win_right: int = 0,
+    layout_q: str = "BSND",
+    layout_kv: str = "PA_ND",
+    has_ori_kv: bool = True,
+    has_cmp_kv: bool = True,
+    aic_core_num: int = 24,
+    aiv_core_num: int = 48,
+    device: Optional[str] = None,
+) -> torch.Tensor:
+    """Generate the scheduling metadata (reference metadata.py:1018-1086).
+
+    Returns the int32[1024] table for ``aic_core_num <= 36``; otherwise the
+    device-resident split-KV plan for ``aic_core_num`` compute units.
+    ``cu_seqlens_cmp_kv`` is accepted for parity and unused, as in the reference.
+    """
+    del cu_seqlens_cmp_kv
+    if aic_core_num <= AIC_CORE_NUM:
+        out = legacy_table(
+            num_heads_q=num_heads_q, num_heads_kv=num_heads_kv, head_dim=head_dim,
+            cu_seqlens_q=cu_seqlens_q, cu_seqlens_ori_kv=cu_seqlens_ori_kv, seqused_q=seqused_q,
+            seqused_kv=seqused_kv, batch_size=batch_size, max_seqlen_q=max_seqlen_q,
+            max_seqlen_kv=max_seqlen_kv, ori_topk=ori_topk, cmp_topk=cmp_topk,
+            cmp_ratio=cmp_ratio, ori_mask_mode=ori_mask_mode, cmp_mask_mode=cmp_mask_mode,
+            ori_win_left=ori_win_left, ori_win_right=ori_win_right, layout_q=layout_q,
+            layout_kv=layout_kv, has_ori_kv=has_ori_kv, has_cmp_kv=has_cmp_kv,
+            aic_core_num=aic_core_num, aiv_core_num=aiv_core_num)
+        return out.to(device) if device is not None else out
+
+    # ---- split-KV plan for all CUs ----
+    if num_heads_kv != 1:
+        raise ValueError(f"only num_heads_kv=1 supported (got {num_heads_kv})")
+    if seqused_kv is None:
+        raise ValueError("seqused_kv is required for the split-KV plan")
+    dev = torch.device(device) if device is not None else (
+        seqused_kv.device if seqused_kv.is_cuda else torch.device("cuda"))
+    if layout_q == "TND":
+        if cu_seqlens_q is None:
+            raise ValueError("cu_seqlens_q is required for TND")
+        cu = cu_seqlens_q.to(dev, torch.int32)
+        batch = cu.numel() - 1
+        total = int(cu[-1].item())  # the token count sizes the plan
+        q_prefix, act_q = cu[:-1], cu[1:] - cu[:-1]
+    else:
+        batch = batch_size if batch_size > 0 else seqused_kv.numel()
+        total = batch * max_seqlen_q
+        q_prefix = torch.arange(batch, dtype=torch.int32, device=dev) * max_seqlen_q
+        act_q = torch.full((batch,), max_seqlen_q, dtype=torch.int32, device=dev)
+        if seqused_q is not None and seqused_q.numel() > 0:
+            act_q = seqused_q.to(dev, torch.int32)
+    scenario = 1 if not has_cmp_kv else (3 if cmp_topk > 0 else 2)
+    p = plan_params(total_tokens=total, batch=batch, num_heads_q=num_heads_q, scenario=scenario,
+                    topk=cmp_topk, cmp_ratio=cmp_ratio, ori_win_left=ori_win_left,
+                    core_num=aic_core_num, head_dim=head_dim)
+    return device_plan(p, q_prefix, act_q, seqused_kv.to(dev))

@@ -1,0 +1,172 @@
+/*
+ * sas.h -- C ABI of the MI355X (gfx950) sparse shared-KV attention library
+ * (libsas_hip.so).
+ *
+ * The operator: DeepSeek-V4-style attention of H query heads over ONE shared
+ * KV head.  Each query token attends (a) a causal sliding window of raw paged
+ * KV rows and (b) compressed paged KV rows -- all causally valid ones
+ * (scenario 2) or a per-token top-k index list (scenario 3) -- through one
+ * online softmax seeded by a per-head sink logit.  K and V are the same row:
+ * V is its first d_v columns.
+ *
+ * Reference interfaces replaced (yangqiang2018/dsv4_planB):
+ *   sas_forward         <- sparse_attn_sharedkv_tilelang/api.py:129-397
+ *                          (api.sparse_attn_sharedkv) and the kernel it
+ *                          launches, kernel.py:62-1268
+ *                          (build_sparse_attn_sharedkv -> func(11 tensors));
+ *                          the 11 tensors map onto sas_tensors_t below
+ *                          (api.py:372-384).
+ *   sas_plan            <- metadata.py:1018-1086 (sparse_attn_sharedkv_metadata)
+ *                          as a GPU split-KV scheduler for all CUs.
+ *   sas_metadata_legacy <- metadata.py:1018-1086 exactly: the int32[1024]
+ *                          FA/FD table for <= 36 cores (metadata.py:38-68,
+ *                          974-1009).
+ *   sas_graph_*         <- the NPUGraph capture/replay of test_graph_mode.py:185-209.
+ *   error codes         <- the reference's AssertionError / ValueError /
+ *                          NotImplementedError guards (api.py:187-191,279-282,
+ *                          362-364; kernel.py:96-108).
+ *
+ * Conventions: all tensor pointers are DEVICE pointers owned by the caller;
+ * every entry point is asynchronous on the given stream, performs no host
+ * synchronisation and no allocation, and is safe to capture into a hipGraph.
+ * Return value 0 = success, negative = sas_status_t error (no launch done).
+ */
+#ifndef SAS_H_
+#define SAS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* sas_stream_t; /* == hipStream_t */
+
+typedef enum {
+  SAS_OK = 0,
+  SAS_ERR_NULL = -1,          /* a required pointer is NULL */
+  SAS_ERR_SHAPE = -2,         /* inconsistent or unsupported shape */
+  SAS_ERR_DTYPE = -3,         /* unsupported dtype combination */
+  SAS_ERR_SCENARIO = -4,      /* scenario not in {1,2,3} or inputs missing for it */
+  SAS_ERR_MASK_MODE = -5,     /* mask modes / window other than the supported ones */
+  SAS_ERR_HEADS = -6,         /* num_heads_kv != 1 or num_heads_q out of range */
+  SAS_ERR_WORKSPACE = -7,     /* workspace too small */
+  SAS_ERR_PLAN = -8,          /* plan buffer too small or not a plan */
+  SAS_ERR_LAUNCH = -9,        /* HIP launch error */
+  SAS_ERR_METADATA = -10,     /* legacy metadata arguments invalid */
+  SAS_ERR_GRAPH = -11,        /* graph capture / instantiate failed */
+  SAS_ERR_NOT_IMPLEMENTED = -12
+} sas_status_t;
+
+typedef enum { SAS_DT_BF16 = 1, SAS_DT_FP16 = 2, SAS_DT_FP8E4M3 = 3 } sas_dtype_t;
+
+typedef struct {
+  int32_t batch;             /* B */
+  int32_t total_tokens;      /* T: rows of q / out */
+  int32_t num_heads_q;       /* H (N1): 1..128 */
+  int32_t num_heads_kv;      /* N2: must be 1 */
+  int32_t head_dim_qk;       /* 512 or 576 */
+  int32_t head_dim_v;        /* 512 (<= head_dim_qk) */
+  int32_t ori_block_num, ori_block_size, ori_table_len;
+  int32_t cmp_block_num, cmp_block_size, cmp_table_len;
+  int64_t ori_block_stride;  /* elements between pages of ori_kv (>= block_size*row_stride) */
+  int64_t ori_row_stride;    /* elements between rows of a page (>= head_dim_qk) */
+  int64_t cmp_block_stride, cmp_row_stride;
+  int32_t topk;              /* K: index slots per token (scenario 3) */
+  int32_t cmp_ratio;         /* compression ratio (scenarios 2, 3) */
+  int32_t scenario;          /* 1 SWA, 2 CFA, 3 SCFA */
+  int32_t ori_win_left;      /* 0..127 (reference: 127) */
+  int32_t ori_win_right;     /* must be 0 */
+  int32_t ori_mask_mode;     /* must be 4 (band) */
+  int32_t cmp_mask_mode;     /* must be 3 */
+  int32_t q_dtype;           /* sas_dtype_t: BF16 or FP16 (out has the same dtype) */
+  int32_t kv_dtype;          /* sas_dtype_t: same as q_dtype, or FP8E4M3 with scales */
+  float softmax_scale;
+  int32_t num_cus;           /* compute units to balance over (0 = query device) */
+  int32_t units_per_cu;      /* split-KV work units targeted per CU (0 = default) */
+} sas_params_t;
+
+typedef struct {
+  const void* q;                    /* [T, H, head_dim_qk]                       */
+  const void* ori_kv;               /* paged [ori_block_num, block_size, 1, Dqk] */
+  const int32_t* ori_block_table;   /* [B, ori_table_len], -1 = unused           */
+  const void* cmp_kv;               /* paged [cmp_block_num, ...] or NULL (SWA)  */
+  const int32_t* cmp_block_table;   /* [B, cmp_table_len] or NULL                */
+  const int32_t* cmp_sparse_indices;/* [T, 1, topk] (scenario 3) or NULL         */
+  const int32_t* q_prefix;          /* [B] first token row of batch b            */
+  const int32_t* act_q_lens;        /* [B] query tokens of batch b               */
+  const int32_t* seqused_kv;        /* [B] raw KV length of batch b              */
+  const float* sinks;               /* [H] fp32                                  */
+  const float* ori_kv_scale;        /* [ori_block_num, block_size] fp32 (fp8)    */
+  const float* cmp_kv_scale;        /* [cmp_block_num, block_size] fp32 (fp8)    */
+  void* out;                        /* [T, H, head_dim_v], q_dtype               */
+  float* lse;                       /* [T, H] fp32, or NULL                      */
+} sas_tensors_t;
+
+/* ---- host-only helpers (no GPU needed) ---- */
+const char* sas_strerror(int code);
+int sas_version(void);
+int sas_validate(const sas_params_t* p);
+/* Bytes of device workspace sas_forward needs for these params. */
+int sas_workspace_size(const sas_params_t* p, size_t* bytes);
+/* int32 entries of the split-KV plan for these params. */
+int sas_plan_size(const sas_params_t* p, size_t* n_int32);
+/* Target number of work units (num_cus * units_per_cu after defaults). */
+int sas_target_units(const sas_params_t* p, int32_t* units);
+
+/* ---- device entry points (asynchronous on stream) ---- */
+/* Split-KV scheduler: per-token row spans and work units balanced over CUs,
+ * from q_prefix / act_q_lens / seqused_kv only (device pointers). */
+int sas_plan(const sas_params_t* p, const int32_t* q_prefix, const int32_t* act_q_lens,
+             const int32_t* seqused_kv, int32_t* plan, size_t plan_n_int32, sas_stream_t stream);
+/* Full forward: (plan if plan == NULL) -> index resolution -> attention ->
+ * split combine.  plan may be a buffer filled by sas_plan for the same params
+ * and lengths. */
+int sas_forward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
+                void* workspace, size_t workspace_bytes, sas_stream_t stream);
+/* The stages of sas_forward, for timing and debugging (same workspace). */
+int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
+                void* workspace, size_t workspace_bytes, sas_stream_t stream);
+int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
+               void* workspace, size_t workspace_bytes, sas_stream_t stream);
+int sas_combine(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
+                void* workspace, size_t workspace_bytes, sas_stream_t stream);
+/* Debug: copy the resolved row-code lists of every token into rows (int32
+ * [T, win_left + 1 (+ topk in scenario 3)]: window pool rows, then compressed pool
+ * rows; -1 = a row read as zeros) and the compressed-row counts into counts [T]. */
+int sas_debug_rows(const sas_params_t* p, const void* workspace, int32_t* rows, int32_t* counts,
+                   sas_stream_t stream);
+
+/* ---- hipGraph capture of sas_forward ---- */
+int sas_graph_capture(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
+                      void* workspace, size_t workspace_bytes, sas_stream_t stream,
+                      void** graph_exec);
+int sas_graph_launch(void* graph_exec, sas_stream_t stream);
+int sas_graph_destroy(void* graph_exec);
+
+/* ---- reference metadata table (host) ---- */
+#define SAS_META_SIZE 1024
+#define SAS_AIC_CORE_NUM 36
+#define SAS_AIV_CORE_NUM 72
+typedef struct {
+  int32_t num_heads_q, num_heads_kv, head_dim;
+  int32_t batch_size, max_seqlen_q, max_seqlen_kv;
+  int32_t ori_topk, cmp_topk, cmp_ratio;
+  int32_t ori_mask_mode, cmp_mask_mode, ori_win_left, ori_win_right;
+  int32_t layout_q;   /* 0 BSND, 1 TND, 2 BSH */
+  int32_t layout_kv;  /* 0 PA_ND, 1 TND */
+  int32_t has_ori_kv, has_cmp_kv;
+  int32_t aic_core_num, aiv_core_num;
+} sas_meta_args_t;
+/* Host arrays; any of them may be NULL (n == 0) as in the reference. */
+int sas_metadata_legacy(const sas_meta_args_t* a, const int32_t* cu_seqlens_q, int32_t n_cu_q,
+                        const int32_t* cu_seqlens_ori_kv, int32_t n_cu_kv,
+                        const int32_t* seqused_q, int32_t n_seqused_q,
+                        const int32_t* seqused_kv, int32_t n_seqused_kv,
+                        int32_t* out /* [SAS_META_SIZE] */);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SAS_H_ */

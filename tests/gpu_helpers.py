@@ -1,0 +1,77 @@
+"""Helpers for the GPU parity tests: numpy case -> device tensors -> operator."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from tests.cases import Case, baseline_tolerance, check_lse_rule, check_result_rule
+
+TORCH_DT = {"bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+def to_device(case: Case, device="cuda"):
+    """Device tensors in the operator's API layout (TND, paged [NB, BS, 1, D])."""
+    qdt = TORCH_DT[case.q_dtype]
+
+    def payload(a, dt):
+        if dt == "fp8e4m3":
+            return torch.from_numpy(a).view(torch.float8_e4m3fn)
+        return torch.from_numpy(a.view(np.int16)).view(TORCH_DT[dt])
+
+    d = dict(
+        q=payload(case.q_bits, case.q_dtype).to(device),
+        ori_kv=payload(case.ori_kv, case.kv_dtype).unsqueeze(2).to(device),
+        ori_block_table=torch.from_numpy(case.ori_block_table).to(device),
+        cu_seqlens_q=torch.from_numpy(case.cu_seqlens_q).to(device),
+        seqused_kv=torch.from_numpy(case.seqused_kv).to(device),
+        sinks=torch.from_numpy(case.sinks).to(device),
+    )
+    if case.cmp_kv is not None:
+        d["cmp_kv"] = payload(case.cmp_kv, case.kv_dtype).unsqueeze(2).to(device)
+        d["cmp_block_table"] = torch.from_numpy(case.cmp_block_table).to(device)
+    if case.idx is not None:
+        d["cmp_sparse_indices"] = torch.from_numpy(case.idx).reshape(case.T, 1, -1).to(device)
+    if case.kv_dtype == "fp8e4m3":
+        d["ori_kv_scale"] = torch.from_numpy(case.ori_scale).unsqueeze(2).to(device)
+        if case.cmp_scale is not None:
+            d["cmp_kv_scale"] = torch.from_numpy(case.cmp_scale).unsqueeze(2).to(device)
+    assert qdt == d["q"].dtype
+    return d
+
+
+def run_op(case: Case, device="cuda", **extra):
+    from dsv4_planb_amd import sparse_attn_sharedkv
+
+    d = to_device(case, device)
+    q = d.pop("q")
+    out, lse = sparse_attn_sharedkv(
+        q, softmax_scale=case.softmax_scale,
+        cmp_ratio=case.cmp_ratio if case.scenario >= 2 else None,
+        ori_win_left=case.win_left, layout_q="TND", return_softmax_lse=True,
+        topk_cmp=case.K if case.scenario == 3 else None, **d, **extra)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), lse.cpu().numpy()
+
+
+def assert_parity(out, lse, ref_out, ref_lse, dtype="bf16", max_abs=2e-2, mean_abs=2e-3,
+                  label=""):
+    """The benchmark tolerance (max-abs 2e-2, mean-abs 2e-3 on bf16 outputs) plus
+    the reference's own check_result / LSE rules."""
+    assert np.isfinite(out).all(), f"{label}: non-finite output"
+    mx, mn = baseline_tolerance(out, ref_out)
+    ful, rel = check_result_rule(out, ref_out, dtype)
+    lful, lrel = check_lse_rule(lse, ref_lse, dtype)
+    msg = (f"{label}: max_abs={mx:.3e} mean_abs={mn:.3e} check_result={ful:.3f}%/{rel:.2f} "
+           f"lse={lful:.3f}%/{lrel:.2f}")
+    print(msg, flush=True)
+    assert mx <= max_abs and mn <= mean_abs, msg
+    assert ful >= 99.5 and rel < 10.0, msg
+    assert lful >= 99.5 and lrel < 10.0, msg
+    return mx, mn
+
+
+def softmax_scale_for(D):
+    return 1.0 / math.sqrt(D)

@@ -1,0 +1,74 @@
+"""The C ABI without a GPU: the library loads, exports every symbol
+``include/sas.h`` declares, and its host-side validation returns the status
+codes that mirror the reference's guards (api.py:187-191, 279-282;
+kernel.py:96-108)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from dsv4_planb_amd import _lib
+from dsv4_planb_amd.metadata import plan_params
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "sas.h")
+
+
+def _declared():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(sas_[a-z_]+)\s*\(", txt)))
+
+
+def test_header_and_exports_agree():
+    lib = _lib.load()
+    names = _declared()
+    assert set(names) == set(_lib.SYMBOLS), (names, _lib.SYMBOLS)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def _good(**kw):
+    p = plan_params(total_tokens=4, batch=2, num_heads_q=64, scenario=3, topk=512, cmp_ratio=4,
+                    ori_win_left=127, core_num=256)
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("num_heads_kv", 2, -6), ("num_heads_q", 0, -6), ("num_heads_q", 129, -6),
+    ("scenario", 4, -4), ("ori_mask_mode", 3, -5), ("ori_win_right", 1, -5),
+    ("cmp_mask_mode", 1, -5), ("q_dtype", 3, -3), ("kv_dtype", 2, -3),
+    ("head_dim_qk", 640, -2), ("head_dim_v", 256, -2), ("batch", 0, -2),
+    ("ori_row_stride", 500, -2), ("topk", 0, -4), ("cmp_ratio", 0, -4),
+])
+def test_validation_codes(field, value, code):
+    lib = _lib.load()
+    assert lib.sas_validate(ctypes.byref(_good())) == 0
+    assert lib.sas_validate(ctypes.byref(_good(**{field: value}))) == code
+    assert lib.sas_strerror(code).decode() not in ("", "unknown error")
+
+
+def test_sizes_and_plan_never_1024():
+    lib = _lib.load()
+    p = _good()
+    ws = ctypes.c_size_t()
+    assert lib.sas_workspace_size(ctypes.byref(p), ctypes.byref(ws)) == 0 and ws.value > 0
+    for T in range(0, 200):
+        for cores in (1, 3, 12, 24, 256):
+            q = _good(total_tokens=T, num_cus=cores)
+            n = ctypes.c_size_t()
+            assert lib.sas_plan_size(ctypes.byref(q), ctypes.byref(n)) == 0
+            assert n.value != 1024
+
+
+def test_null_arguments_rejected_without_launch():
+    lib = _lib.load()
+    p = _good()
+    t = _lib.SasTensors()
+    assert lib.sas_forward(ctypes.byref(p), ctypes.byref(t), None, None, 0, None) == -1
+    assert lib.sas_plan(ctypes.byref(p), None, None, None, None, 0, None) == -1
+    assert lib.sas_graph_launch(None, None) == -1

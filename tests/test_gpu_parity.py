@@ -1,0 +1,165 @@
+"""GPU parity: the HIP path through the C ABI versus the oracle.
+
+Each case prints its name and shape before it runs.  Tolerances: the benchmark
+rule (max-abs 2e-2, mean-abs 2e-3 on bf16 outputs) and the reference's own
+check_result / LSE rules (test_sparse_attn_sharedkv.py:394-527).  Gather,
+index and page-table resolution are compared bit-exactly.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from tests.cases import make_case
+from tests.gpu_helpers import assert_parity, run_op, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def _banner(name, c):
+    print(f"\n[case] {name}: B={c.B} T={c.T} H={c.H} D={c.D} scen={c.scenario} K={c.K} "
+          f"kv={c.kv_dtype} q={c.q_dtype}", flush=True)
+
+
+def _check(name, c, tokens=None, **extra):
+    _banner(name, c)
+    out, lse = run_op(c, **extra)
+    ref, ref_lse = c.oracle_c(tokens=tokens)
+    if tokens is not None:
+        out, lse, ref, ref_lse = out[tokens], lse[tokens], ref[tokens], ref_lse[tokens]
+    return assert_parity(out, lse, ref, ref_lse, dtype=c.q_dtype, label=name)
+
+
+# ---- benchmark configurations (full size where the oracle is quick) ----
+def test_c1_swa_decode():
+    c = make_case(B=2, H=16, seq_kv=[1024, 1024], q_per_seq=1, scenario=1, seed=1)
+    _check("c1", c)
+
+
+def test_c2_decode_topk512_full():
+    rng = np.random.default_rng(2)
+    kv = rng.integers(4096, 32769, size=32).tolist()
+    c = make_case(B=32, H=64, seq_kv=kv, q_per_seq=1, scenario=3, K=512, seed=2)
+    _check("c2", c)
+
+
+def test_c3_shape_mtp2_topk2048_reduced_batch():
+    c = make_case(B=3, H=128, seq_kv=[131072] * 3, q_per_seq=2, scenario=3, K=2048, seed=3)
+    _check("c3[B=3]", c)
+
+
+def test_c4_shape_prefill_reduced_tokens():
+    c = make_case(B=1, H=128, seq_kv=[1024], q_per_seq=1024, scenario=3, K=2048, seed=4)
+    toks = list(range(0, 1024, 7)) + [1023]
+    _check("c4[T=1024]", c, tokens=toks)
+
+
+def test_c5_ragged_fp8_reduced():
+    rng = np.random.default_rng(5)
+    B = 8
+    kv = np.exp(rng.uniform(np.log(256), np.log(131072), size=B)).astype(int).tolist()
+    qn = rng.choice([1, 2, 4], size=B).tolist()
+    c = make_case(B=B, H=128, seq_kv=kv, q_per_seq=qn, scenario=3, K=2048, kv_dtype="fp8e4m3",
+                  seed=5)
+    _check("c5[B=8,fp8]", c)
+
+
+# ---- reference scenarios (test_sparse_attn_sharedkv.py:81-220): D=512, H=64, page 128,
+# U(-10,10) queries / raw KV as in the reference generators; prefills at S1=1024 as in
+# test_sparse_attn_sharedkv_fast.py ----
+def _ref_case(scenario, s1, kv, ratio, K, D=512, seed=42):
+    c = make_case(B=1, H=64, D=D, seq_kv=[kv], q_per_seq=s1, scenario=scenario, K=K,
+                  cmp_ratio=ratio, block_size=128, cmp_block_size=128, seed=seed,
+                  softmax_scale=0.04419417, value_scale=5.0)
+    return c
+
+
+@pytest.mark.parametrize("name,scen,s1,kv,ratio,K", [
+    ("scfa_decode", 3, 1, 8193, 4, 512), ("swa_decode", 1, 1, 8193, 4, 0),
+    ("cfa_decode", 2, 1, 8193, 128, 0), ("scfa_prefill_fast", 3, 1024, 1024, 4, 512),
+    ("swa_prefill_fast", 1, 1024, 1024, 4, 0), ("cfa_prefill_fast", 2, 1024, 1024, 128, 0),
+])
+def test_reference_scenarios(name, scen, s1, kv, ratio, K):
+    c = _ref_case(scen, s1, kv, ratio, K)
+    toks = None if s1 == 1 else list(range(0, s1, 5)) + [s1 - 1]
+    _check(name, c, tokens=toks)
+
+
+def test_fp16_scfa():
+    c = make_case(B=3, H=64, seq_kv=[3000, 700, 9000], q_per_seq=[1, 2, 3], scenario=3, K=512,
+                  q_dtype="fp16", kv_dtype="fp16", seed=6)
+    _check("fp16", c)
+
+
+def test_d512_scfa_h128():
+    c = make_case(B=2, H=128, D=512, seq_kv=[5000, 12000], q_per_seq=2, scenario=3, K=1024, seed=7)
+    _check("d512", c)
+
+
+# ---- edge cases the reference semantics define ----
+def test_edges_terminator_threshold_padding_and_empty():
+    c = make_case(B=4, H=32, seq_kv=[900, 3000, 2, 64], q_per_seq=[2, 3, 3, 1], scenario=3, K=256,
+                  seed=8)
+    c.idx[0, 3] = -1              # -1 terminates the list
+    c.idx[1, 0] = 10_000          # beyond the threshold: skipped
+    c.idx[1, 5] = int(c.idx[1, 4])  # duplicates are kept
+    # batch 2: act_kv=2 < act_q=3 -> first token has s_global < 0 (no rows at all)
+    _check("edges", c)
+
+
+def test_h16_padded_heads_and_many_splits():
+    c = make_case(B=2, H=16, seq_kv=[20000, 4000], q_per_seq=1, scenario=3, K=2048, seed=9)
+    _check("splits", c, core_num=256, units_per_cu=0)
+
+
+def test_sink_minus_inf_and_large_logits():
+    c = make_case(B=2, H=32, seq_kv=[5000, 800], q_per_seq=2, scenario=3, K=512, seed=10,
+                  value_scale=3.0)
+    c.sinks[:8] = -np.inf
+    _check("sink-inf", c)
+
+
+def test_resolution_bit_exact():
+    """Window and compressed row codes (paged pool rows, -1 = zero row) and the
+    compressed counts equal the oracle's resolution exactly."""
+    from oracle import golden_c
+    from dsv4_planb_amd import _lib
+    from dsv4_planb_amd.api import build_launch
+
+    c = make_case(B=5, H=16, seq_kv=[130, 4000, 64, 9000, 2], q_per_seq=[1, 2, 4, 3, 2],
+                  scenario=3, K=300, seed=11)
+    c.idx[2, 1] = -1
+    c.idx[4, 0] = 99_999
+    c.ori_block_table[1, 3] = -1  # an unused page inside the window reads as zeros
+    _banner("resolve", c)
+    d = to_device(c)
+    launch, out, lse = build_launch(
+        q_flat=d["q"], ori_kv=d["ori_kv"], ori_block_table=d["ori_block_table"],
+        cmp_kv=d["cmp_kv"], cmp_block_table=d["cmp_block_table"],
+        cmp_indices=d["cmp_sparse_indices"], q_prefix=d["cu_seqlens_q"][:-1],
+        act_q_lens=d["cu_seqlens_q"][1:] - d["cu_seqlens_q"][:-1], seqused_kv=d["seqused_kv"],
+        sinks=d["sinks"], metadata=None, scenario=3, topk=c.K, cmp_ratio=4, ori_win_left=127,
+        softmax_scale=c.softmax_scale, core_num=256)
+    launch.run()
+    W = 128
+    rows = torch.zeros((c.T, W + c.K), dtype=torch.int32, device="cuda")
+    cnt = torch.zeros(c.T, dtype=torch.int32, device="cuda")
+    rc = _lib.load().sas_debug_rows(ctypes.byref(launch.params), ctypes.c_void_p(launch.ws.data_ptr()),
+                                    ctypes.c_void_p(rows.data_ptr()), ctypes.c_void_p(cnt.data_ptr()),
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(rc)
+    torch.cuda.synchronize()
+    rows, cnt = rows.cpu().numpy(), cnt.cpu().numpy()
+    ref, n_ori, n_cmp = golden_c.resolve(
+        T=c.T, ori_block_table=c.ori_block_table, ori_block_size=64, q_prefix=c.q_prefix,
+        act_q=c.act_q, seqused_kv=c.seqused_kv, scenario=3, cmp_block_table=c.cmp_block_table,
+        cmp_block_size=64, cmp_sparse_indices=c.idx)
+    for t in range(c.T):
+        no, nc = int(n_ori[t]), int(n_cmp[t])
+        assert cnt[t] == nc, (t, cnt[t], nc)
+        np.testing.assert_array_equal(rows[t, :no], ref[t, :no])
+        np.testing.assert_array_equal(rows[t, W:W + nc], ref[t, no:no + nc])

@@ -1,0 +1,329 @@
+"""Pins for the oracle (CPU only).
+
+Each check compares the oracle with something it does not contain: the
+reference's known-answer test redone in float64, reduction cases the
+mathematics fixes, brute force over every slot, and planted mistakes that must
+fail those checks.  Reference citations are to
+``sparse_attn_sharedkv_tilelang/{golden.py,test_sparse_attn_sharedkv.py}``.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import golden_ref as G
+from tests.cases import make_case
+
+
+# --------------------------------------------------------------------------
+# Index resolution (golden.py:28-66): brute-force special cases.
+# --------------------------------------------------------------------------
+def test_resolve_threshold_zero_gives_no_rows():
+    # act_kv=7, act_q=1, s=0 -> s_global=6, thr=floor(7/8)=0 with ratio 8
+    assert G.resolve_cmp_ids([0, 1, 2], act_kv=7, act_q=1, s_local=0, cmp_ratio=8) == []
+
+
+def test_resolve_minus_one_terminates_not_skips():
+    ids = G.resolve_cmp_ids([3, -1, 1, 2], act_kv=100, act_q=1, s_local=0, cmp_ratio=4)
+    assert ids == [3]
+
+
+def test_resolve_skips_ids_at_or_beyond_threshold():
+    # thr = floor(100/4) = 25: 25 and 40 skipped, 24 kept, order kept, duplicates kept
+    ids = G.resolve_cmp_ids([25, 24, 40, 0, 24], act_kv=100, act_q=1, s_local=0, cmp_ratio=4)
+    assert ids == [24, 0, 24]
+
+
+def test_resolve_examines_only_first_thr_slots():
+    # thr = floor(12/4) = 3: only slots 0..2 are looked at, slot 3 (valid id 1) ignored
+    ids = G.resolve_cmp_ids([2, 0, 5, 1], act_kv=12, act_q=1, s_local=0, cmp_ratio=4)
+    assert ids == [2, 0]
+
+
+def test_resolve_mtp_thresholds_follow_token_position():
+    # act_kv=16, act_q=2: s=0 -> s_global=14 thr=3; s=1 -> s_global=15 thr=4
+    row = [3, 2, 1, 0]
+    assert G.resolve_cmp_ids(row, act_kv=16, act_q=2, s_local=0, cmp_ratio=4) == [2, 1]
+    assert G.resolve_cmp_ids(row, act_kv=16, act_q=2, s_local=1, cmp_ratio=4) == [3, 2, 1, 0]
+
+
+def test_resolve_rejects_out_of_contract_negative_ids():
+    with pytest.raises(ValueError):
+        G.resolve_cmp_ids([-2], act_kv=100, act_q=1, s_local=0, cmp_ratio=4)
+
+
+def test_window_positions_edges():
+    assert list(G.window_positions(0)) == [0]
+    assert list(G.window_positions(5)) == list(range(0, 6))
+    assert list(G.window_positions(127)) == list(range(0, 128))
+    assert list(G.window_positions(200)) == list(range(73, 201))
+    assert list(G.window_positions(-1)) == []
+
+
+def test_paged_row_matches_dense_unpack_every_slot():
+    rng = np.random.default_rng(3)
+    B, BS, D, NB = 3, 4, 2, 16
+    pool = rng.standard_normal((NB, BS, D)).astype(np.float32)
+    bt = np.full((B, 5), -1, np.int32)
+    perm = rng.permutation(NB)
+    bt[0, :3] = perm[:3]
+    bt[1, :5] = perm[3:8]
+    bt[2, [0, 2]] = perm[8:10]  # a hole at logical page 1
+    dense = G.unpack_paged(pool, bt, 20)
+    flat = pool.reshape(-1, D)
+    for b in range(B):
+        for p in range(20):
+            r = G.paged_row(bt[b], p, BS)
+            want = dense[b, p]
+            got = np.zeros(D, np.float32) if r < 0 else flat[r]
+            np.testing.assert_array_equal(got, want)
+
+
+def test_c_resolve_matches_numpy_resolve():
+    from oracle import golden_c
+
+    c = make_case(B=3, H=4, seq_kv=[300, 1100, 70], q_per_seq=[1, 3, 2], K=64, seed=5)
+    # plant -1 early and ids beyond the threshold in a few rows
+    c.idx[1, 5] = -1
+    c.idx[2, 0] = 10_000
+    rows, n_ori, n_cmp = golden_c.resolve(
+        T=c.T, ori_block_table=c.ori_block_table, ori_block_size=64, q_prefix=c.q_prefix,
+        act_q=c.act_q, seqused_kv=c.seqused_kv, scenario=3,
+        cmp_block_table=c.cmp_block_table, cmp_block_size=64, cmp_sparse_indices=c.idx)
+    for b in range(c.B):
+        for s in range(int(c.act_q[b])):
+            t = int(c.q_prefix[b]) + s
+            o, cm = G.token_rows(b=b, s_local=s, act_q=int(c.act_q[b]),
+                                 act_kv=int(c.seqused_kv[b]), scenario=3,
+                                 ori_block_table=c.ori_block_table, ori_block_size=64,
+                                 cmp_block_table=c.cmp_block_table, cmp_block_size=64,
+                                 idx_row=c.idx[t], cmp_ratio=4)
+            assert n_ori[t] == len(o) and n_cmp[t] == len(cm)
+            assert list(rows[t, :len(o) + len(cm)]) == o + cm
+
+
+# --------------------------------------------------------------------------
+# Attention math: the reference KAT (test_sparse_attn_sharedkv.py:976-1048)
+# redone against a float64 one-shot softmax.
+# --------------------------------------------------------------------------
+def _kat_case(D, H, seq, S1, K, seed=0, sink_scale=0.1, dense=False):
+    rng = np.random.default_rng(seed)
+    cmp_ratio = 4
+    q = (rng.random((S1, H, D)) * 2 - 1).astype(np.float32)
+    ori = (rng.random((seq, D)) * 2 - 1).astype(np.float32)
+    cmpk = (rng.random((seq // cmp_ratio, D)) * 2 - 1).astype(np.float32)
+    sinks = (rng.random(H) * sink_scale).astype(np.float32)
+    idx = np.full((S1, K), -1, np.int32)
+    for s in range(S1):
+        thr = (seq - S1 + s + 1) // cmp_ratio
+        take = min(K, max(thr, 0))
+        idx[s, :take] = rng.permutation(max(thr, 0))[:take] if not dense else np.arange(take)
+    # a single page holding the whole sequence keeps paging trivial here
+    ori_pool = ori[None]
+    cmp_pool = cmpk[None]
+    return dict(q=q, ori=ori, cmpk=cmpk, sinks=sinks, idx=idx, ori_pool=ori_pool,
+                cmp_pool=cmp_pool, cmp_ratio=cmp_ratio, seq=seq, S1=S1, D=D)
+
+
+def _chunked(kc, q_dtype="fp32", scenario=3, tokens=None):
+    return G.golden_attention(
+        q=kc["q"], ori_kv=kc["ori_pool"], ori_block_table=np.zeros((1, 1), np.int32),
+        q_prefix=[0], act_q=[kc["S1"]], seqused_kv=[kc["seq"]], sinks=kc["sinks"],
+        softmax_scale=1.0 / math.sqrt(kc["D"]), scenario=scenario, cmp_kv=kc["cmp_pool"],
+        cmp_block_table=np.zeros((1, 1), np.int32), cmp_sparse_indices=kc["idx"],
+        cmp_ratio=kc["cmp_ratio"], q_dtype=q_dtype, tokens=tokens)
+
+
+def _one_shot(kc, scenario=3):
+    S1, D = kc["S1"], kc["D"]
+    outs, lses = [], []
+    for s in range(S1):
+        s_g = kc["seq"] - S1 + s
+        ori_k = kc["ori"][max(s_g - 127, 0): s_g + 1]
+        thr = (s_g + 1) // kc["cmp_ratio"]
+        if scenario == 3:
+            raw = kc["idx"][s]
+            # the KAT's own selection: valid = 0 <= id < thr (no -1 in the middle here)
+            sel = raw[(raw >= 0) & (raw < thr)]
+        elif scenario == 2:
+            sel = np.arange(max(thr, 0))
+        else:
+            sel = np.zeros(0, np.int64)
+        k_concat = np.concatenate([ori_k, kc["cmpk"][sel]], axis=0)
+        o, l = G.sinks_softmax_reference_f64(kc["q"][s], k_concat, kc["sinks"],
+                                             1.0 / math.sqrt(D))
+        outs.append(o)
+        lses.append(l)
+    return np.stack(outs), np.stack(lses)
+
+
+@pytest.mark.parametrize("D,H,seq,S1,K", [
+    (512, 64, 128, 4, 8),        # the reference KAT shape
+    (576, 16, 1024, 3, 300),     # d_qk = 576, several cmp rows
+    (576, 8, 4400, 2, 1100),     # > 512 cmp rows: crosses golden's 512-row tile
+])
+def test_kat_chunked_equals_one_shot_f64(D, H, seq, S1, K):
+    kc = _kat_case(D, H, seq, S1, K, seed=D + H)
+    out, lse = _chunked(kc)
+    ref, ref_lse = _one_shot(kc)
+    # fp32 inputs: the benchmark asks for 1e-5 relative agreement
+    rel = np.abs(out - ref).max() / np.abs(ref).max()
+    assert rel < 1e-5, rel
+    np.testing.assert_allclose(lse, ref_lse, rtol=1e-5, atol=1e-5)
+
+
+def test_kat_dense_cmp_scenario2():
+    kc = _kat_case(576, 8, 700, 3, 0, seed=11)
+    out, lse = _chunked(kc, scenario=2)
+    ref, ref_lse = _one_shot(kc, scenario=2)
+    assert np.abs(out - ref).max() / np.abs(ref).max() < 1e-5
+    np.testing.assert_allclose(lse, ref_lse, rtol=1e-5, atol=1e-5)
+
+
+def test_sink_minus_inf_reduces_to_plain_softmax_attention():
+    kc = _kat_case(576, 8, 300, 2, 40, seed=2)
+    kc["sinks"] = np.full(8, -np.inf, np.float32)
+    out, lse = _chunked(kc)
+    for s in range(kc["S1"]):
+        s_g = kc["seq"] - kc["S1"] + s
+        ori_k = kc["ori"][max(s_g - 127, 0): s_g + 1].astype(np.float64)
+        thr = (s_g + 1) // 4
+        raw = kc["idx"][s]
+        k = np.concatenate([ori_k, kc["cmpk"][raw[(raw >= 0) & (raw < thr)]]], axis=0)
+        x = kc["q"][s].astype(np.float64) @ k.T / math.sqrt(576)
+        w = np.exp(x - x.max(axis=1, keepdims=True))
+        w /= w.sum(axis=1, keepdims=True)
+        np.testing.assert_allclose(out[s], w @ k, rtol=0, atol=2e-6)
+        np.testing.assert_allclose(lse[s], np.log(np.exp(x).sum(axis=1)), rtol=1e-6)
+
+
+def test_single_key_gives_v_and_logaddexp_lse():
+    # act_kv = act_q = 1 -> window = {0}, thr = floor(1/4) = 0: exactly one key
+    rng = np.random.default_rng(9)
+    D, H = 576, 4
+    q = rng.standard_normal((1, H, D)).astype(np.float32)
+    ori = rng.standard_normal((1, 64, D)).astype(np.float32)
+    sinks = rng.uniform(-1, 1, H).astype(np.float32)
+    out, lse = G.golden_attention(q=q, ori_kv=ori, ori_block_table=np.zeros((1, 1), np.int32),
+                                  q_prefix=[0], act_q=[1], seqused_kv=[1], sinks=sinks,
+                                  softmax_scale=0.05, scenario=1, q_dtype="fp32")
+    s = (q[0].astype(np.float64) @ ori[0, 0].astype(np.float64)) * 0.05
+    w = np.exp(s - np.logaddexp(s, sinks))
+    np.testing.assert_allclose(out[0], w[:, None] * ori[0, 0][None, :], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(lse[0], np.logaddexp(s, sinks), rtol=1e-6)
+
+
+def test_no_keys_gives_zero_and_sink_lse():
+    # act_kv=0 with one query token: s_global = -1 -> empty window, thr = 0
+    q = np.ones((1, 3, 8), np.float32)
+    ori = np.ones((1, 4, 8), np.float32)
+    sinks = np.array([0.3, -0.2, 1.0], np.float32)
+    out, lse = G.golden_attention(q=q, ori_kv=ori, ori_block_table=np.zeros((1, 1), np.int32),
+                                  q_prefix=[0], act_q=[1], seqused_kv=[0], sinks=sinks,
+                                  softmax_scale=1.0, scenario=3, cmp_kv=ori,
+                                  cmp_block_table=np.zeros((1, 1), np.int32),
+                                  cmp_sparse_indices=np.zeros((1, 4), np.int32),
+                                  q_dtype="fp32")
+    assert np.all(out == 0)
+    np.testing.assert_array_equal(lse[0], sinks)
+
+
+def _swa_via_band_mask(case):
+    """SWA as dense attention with a banded causal mask (independent of the
+    window slicing): token at s_global attends p with s_global-127 <= p <= s_global."""
+    q = case.q_f32()
+    dense = G.unpack_paged(case.ori_f32(), case.ori_block_table, int(case.seqused_kv.max()))
+    outs = np.zeros((case.T, case.H, case.Dv))
+    for b in range(case.B):
+        akv, aq = int(case.seqused_kv[b]), int(case.act_q[b])
+        pos = np.arange(akv)
+        for s in range(aq):
+            t = int(case.q_prefix[b]) + s
+            s_g = akv - aq + s
+            mask = (pos <= s_g) & (pos >= s_g - 127)
+            k = dense[b, :akv].astype(np.float64)
+            x = q[t].astype(np.float64) @ k.T * case.softmax_scale
+            x = np.where(mask[None, :], x, -np.inf)
+            x = np.concatenate([x, case.sinks[:, None].astype(np.float64)], axis=1)
+            w = np.exp(x - x.max(axis=1, keepdims=True))
+            w /= w.sum(axis=1, keepdims=True)
+            outs[t] = w[:, :-1] @ k[:, :case.Dv]
+    return outs
+
+
+def test_swa_equals_band_mask_attention():
+    c = make_case(B=2, H=16, seq_kv=[1024, 300], q_per_seq=[1, 3], scenario=1, q_dtype="fp32",
+                  kv_dtype="fp32", seed=1)
+    out, _ = c.oracle_numpy()
+    ref = _swa_via_band_mask(c)
+    assert np.abs(out - ref).max() < 1e-5
+
+
+# --------------------------------------------------------------------------
+# Planted mistakes: each must break at least one of the pins above.
+# --------------------------------------------------------------------------
+def test_planted_window_off_by_one_is_caught(monkeypatch):
+    c = make_case(B=1, H=4, seq_kv=[400], q_per_seq=2, scenario=1, q_dtype="fp32",
+                  kv_dtype="fp32", seed=4)
+    monkeypatch.setattr(G, "window_positions",
+                        lambda s_g, win_left=127, win_right=0: range(max(s_g - win_left - 1, 0), s_g + 1))
+    out, _ = c.oracle_numpy()
+    assert np.abs(out - _swa_via_band_mask(c)).max() > 1e-3
+
+
+def test_planted_dropped_sink_is_caught(monkeypatch):
+    kc = _kat_case(576, 8, 300, 2, 40, seed=6, sink_scale=2.0)
+    real = G.online_softmax_rows
+
+    def no_sink(q, ori_k, cmp_k, sinks, scale, p_dtype, s2_tile=512):
+        return real(q, ori_k, cmp_k, np.full_like(sinks, -np.inf), scale, p_dtype, s2_tile)
+
+    monkeypatch.setattr(G, "online_softmax_rows", no_sink)
+    out, lse = _chunked(kc)
+    ref, ref_lse = _one_shot(kc)
+    assert np.abs(lse - ref_lse).max() > 1e-3
+
+
+def test_planted_minus_one_skip_instead_of_break_is_caught():
+    row = [3, -1, 1, 2]
+
+    def mutated(idx_row, *, act_kv, act_q, s_local, cmp_ratio):
+        thr = math.floor((act_kv - act_q + s_local + 1) / cmp_ratio)
+        return [int(x) for x in idx_row[:min(len(idx_row), thr)] if 0 <= x < thr]
+
+    assert mutated(row, act_kv=100, act_q=1, s_local=0, cmp_ratio=4) != [3]
+    assert G.resolve_cmp_ids(row, act_kv=100, act_q=1, s_local=0, cmp_ratio=4) == [3]
+
+
+def test_planted_missing_p_rounding_changes_bf16_result(monkeypatch):
+    c = make_case(B=1, H=8, seq_kv=[2000], q_per_seq=1, K=600, seed=8)
+    out_ok, _ = c.oracle_numpy()
+    monkeypatch.setattr(G, "round_to", lambda x, dt: np.asarray(x, np.float32) if dt != "bf16" or x.ndim == 2 else G.round_bf16(x))
+    out_bad, _ = c.oracle_numpy()
+    # the output cast survives; only the P cast is dropped -- a visible but small change
+    assert np.abs(out_ok - out_bad).max() > 0
+
+
+# --------------------------------------------------------------------------
+# C oracle == numpy oracle.
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("kw", [
+    dict(B=2, H=16, seq_kv=[1024, 1024], q_per_seq=1, scenario=1),
+    dict(B=3, H=8, seq_kv=[700, 2500, 90], q_per_seq=[1, 2, 4], scenario=3, K=640),
+    dict(B=2, H=8, seq_kv=[1500, 333], q_per_seq=[2, 1], scenario=2),
+    dict(B=2, H=4, seq_kv=[900, 2100], q_per_seq=[1, 2], scenario=3, K=256, kv_dtype="fp8e4m3"),
+    dict(B=1, H=4, seq_kv=[600], q_per_seq=3, scenario=3, K=128, q_dtype="fp16", kv_dtype="fp16"),
+    dict(B=1, H=4, seq_kv=[600], q_per_seq=2, scenario=3, K=128, D=512, Dv=512),
+])
+def test_c_oracle_matches_numpy_oracle(kw):
+    c = make_case(seed=21, **kw)
+    o_np, l_np = c.oracle_numpy()
+    o_c, l_c = c.oracle_c(nthreads=2)
+    tol = 1e-2 if c.q_dtype != "fp32" else 1e-5  # one low-precision ulp of the output
+    assert np.abs(o_np - o_c).max() <= tol * max(1.0, np.abs(o_np).max())
+    np.testing.assert_allclose(l_np, l_c, rtol=1e-5, atol=1e-5)
+    # almost every element identical (summation order is the only difference)
+    assert np.mean(o_np == o_c) > 0.97
