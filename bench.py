@@ -118,6 +118,10 @@ def make_workload(name: str, seed: int = 0, dev="cuda"):
 # ---------------------------------------------------------------------------
 # GPU timing
 # ---------------------------------------------------------------------------
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def _events_time(fn, n, stream):
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -304,8 +308,11 @@ def main():
     dev = torch.device("cuda:0")
     results = {}
     for name in [args.workload] + [w for w in args.extra.split(",") if w and w != args.workload]:
+        _log(f"{name}: building inputs")
         wl = make_workload(name, seed=0, dev=dev)
+        _log(f"{name}: timing")
         r = measure(wl, args.steps, args.warmup)
+        _log(f"{name}: call {r['call_us']:.1f} us, attend {r['attend_us']:.1f} us")
         attend_s = r["attend_us"] * 1e-6
         r.update(alg_bytes=wl["alg_bytes"], alg_flops=wl["alg_flops"], uniq_rows=wl["uniq_rows"],
                  rows_total=wl["rows_total"],
@@ -329,6 +336,7 @@ def main():
                 "algorithmic_bytes": main_r["alg_bytes"], "algorithmic_flops": main_r["alg_flops"]}
     cpu = None
     if not args.no_cpu_baseline:
+        _log("cpu baseline")
         if args.workload == "prefill8k":
             cpu = cpu_baseline(args.workload, 1)
         else:  # size the sample for ~10 s of CPU work, from a one-sequence probe

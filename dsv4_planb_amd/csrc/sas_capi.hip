@@ -7,11 +7,13 @@
 // device memory or synchronises the host.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
 #include "sas_common.h"
 #include "sas_kernels.hip"
+#include "sas_attend.hip"
 
 namespace {
 
@@ -95,6 +97,8 @@ struct Ws {
   int* plan;
   float* o;
   float* ml;
+  int* flags;
+  float* redo_m;
 };
 
 int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out) {
@@ -109,6 +113,8 @@ int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out)
   out->plan = reinterpret_cast<int*>(base + W.off_plan);
   out->o = reinterpret_cast<float*>(base + W.off_o);
   out->ml = reinterpret_cast<float*>(base + W.off_ml);
+  out->flags = reinterpret_cast<int*>(base + W.off_flags);
+  out->redo_m = reinterpret_cast<float*>(base + W.off_redo_m);
   return SAS_OK;
 }
 
@@ -139,6 +145,22 @@ fwd_fn_t pick_fwd(const sas_params_t* p) {
   if (nw <= 1) return pick_dqk<1>(p->head_dim_qk, qt, kv8);
   if (nw == 2) return pick_dqk<2>(p->head_dim_qk, qt, kv8);
   return pick_dqk<4>(p->head_dim_qk, qt, kv8);
+}
+
+typedef void (*attend_fn_t)(SasFwdArgs, const uint16_t*, const uint8_t*, const uint8_t*,
+                            const int*, const int*, const int*, const float*, const int*,
+                            uint16_t*, float*, float*, float*, int*, float*);
+
+attend_fn_t pick_attend(const sas_params_t* p, bool redo) {
+  const bool f16 = p->q_dtype == SAS_DT_FP16;
+  if (redo) {
+    if (p->head_dim_qk == 576)
+      return f16 ? &sas::attend_redo_kernel<576, 1> : &sas::attend_redo_kernel<576, 0>;
+    return f16 ? &sas::attend_redo_kernel<512, 1> : &sas::attend_redo_kernel<512, 0>;
+  }
+  if (p->head_dim_qk == 576)
+    return f16 ? &sas::attend_kernel<576, 1> : &sas::attend_kernel<576, 0>;
+  return f16 ? &sas::attend_kernel<512, 1> : &sas::attend_kernel<512, 0>;
 }
 
 int launch_status() { return hipGetLastError() == hipSuccess ? SAS_OK : SAS_ERR_LAUNCH; }
@@ -251,7 +273,7 @@ int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   if (p->total_tokens == 0) return SAS_OK;
   hipLaunchKernelGGL(sas::resolve_kernel, dim3(p->total_tokens), dim3(64), 0, (hipStream_t)stream,
                      fwd_args(p, target), plan, t->ori_block_table, t->cmp_sparse_indices,
-                     t->cmp_block_table, w.rows, w.ncmp);
+                     t->cmp_block_table, w.rows, w.ncmp, w.flags);
   return launch_status();
 }
 
@@ -266,6 +288,22 @@ int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pla
   if (!plan) plan = w.plan;
   if (p->total_tokens == 0) return SAS_OK;
   const SasFwdArgs a = fwd_args(p, target);
+  if (p->kv_dtype != SAS_DT_FP8E4M3) {
+    // first pass, then the redo pass for units whose logits outgrew their frame
+    const int redo_grid = std::min(a.unit_cap, std::max(1, query_num_cus()));
+    for (int redo = 0; redo < 2; ++redo) {
+      attend_fn_t fn = pick_attend(p, redo != 0);
+      hipLaunchKernelGGL(fn, dim3(redo ? redo_grid : a.unit_cap), dim3(256), 0,
+                         (hipStream_t)stream, a,
+                         static_cast<const uint16_t*>(t->q),
+                         static_cast<const uint8_t*>(t->ori_kv),
+                         static_cast<const uint8_t*>(t->cmp_kv), t->cmp_block_table, w.rows,
+                         w.ncmp, t->sinks, plan, static_cast<uint16_t*>(t->out), t->lse, w.o,
+                         w.ml, w.flags, w.redo_m);
+      if ((rc = launch_status())) return rc;
+    }
+    return SAS_OK;
+  }
   fwd_fn_t fn = pick_fwd(p);
   hipLaunchKernelGGL(fn, dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream, a,
                      static_cast<const uint16_t*>(t->q), static_cast<const uint8_t*>(t->ori_kv),
@@ -286,12 +324,14 @@ int sas_combine(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   if (!plan) plan = w.plan;
   if (p->total_tokens == 0) return SAS_OK;
   const SasFwdArgs a = fwd_args(p, target);
+  const dim3 grid(target, (p->num_heads_q + sas::COMBINE_HEADS - 1) / sas::COMBINE_HEADS);
+  const dim3 block(64 * sas::COMBINE_HEADS);
   if (p->q_dtype == SAS_DT_BF16)
-    hipLaunchKernelGGL(sas::combine_kernel<0>, dim3(target), dim3(256), 0, (hipStream_t)stream, a,
-                       plan, w.o, w.ml, static_cast<uint16_t*>(t->out), t->lse);
+    hipLaunchKernelGGL(sas::combine_kernel<0>, grid, block, 0, (hipStream_t)stream, a, plan, w.o,
+                       w.ml, static_cast<uint16_t*>(t->out), t->lse);
   else
-    hipLaunchKernelGGL(sas::combine_kernel<1>, dim3(target), dim3(256), 0, (hipStream_t)stream, a,
-                       plan, w.o, w.ml, static_cast<uint16_t*>(t->out), t->lse);
+    hipLaunchKernelGGL(sas::combine_kernel<1>, grid, block, 0, (hipStream_t)stream, a, plan, w.o,
+                       w.ml, static_cast<uint16_t*>(t->out), t->lse);
   return launch_status();
 }
 
@@ -346,13 +386,13 @@ int sas_graph_capture(const sas_params_t* p, const sas_tensors_t* t, const int32
   rc = sas_forward(p, t, plan, ws, ws_bytes, stream);
   hipError_t e = hipStreamEndCapture(s, &graph);
   if (rc) {
-    if (graph) hipGraphDestroy(graph);
+    if (graph) (void)hipGraphDestroy(graph);
     return rc;
   }
   if (e != hipSuccess || !graph) return SAS_ERR_GRAPH;
   hipGraphExec_t exec = nullptr;
   e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-  hipGraphDestroy(graph);
+  (void)hipGraphDestroy(graph);
   if (e != hipSuccess) return SAS_ERR_GRAPH;
   *graph_exec = exec;
   return SAS_OK;

@@ -54,7 +54,7 @@ SAS_HD static inline SasPlanLayout sas_plan_layout(int64_t T, int64_t target) {
 
 // ---- workspace (bytes, each region 256-B aligned) ----
 struct SasWsLayout {
-  size_t off_rows, off_ncmp, off_plan, off_o, off_ml, total;
+  size_t off_rows, off_ncmp, off_plan, off_o, off_ml, off_flags, off_redo_m, total;
   int64_t slot_cap;
 };
 
@@ -81,8 +81,14 @@ SAS_HD static inline SasWsLayout sas_ws_layout(int64_t T, int64_t K, int64_t H, 
   W.slot_cap = 2 * target;
   W.off_o = off;
   off = sas_align256(off + (size_t)W.slot_cap * H * Dv * 4);
-  W.off_ml = off;
-  off = sas_align256(off + (size_t)W.slot_cap * H * 2 * 4);
+  W.off_ml = off;  // per (slot, head): float4 (m, l_w, l_e, 0)
+  off = sas_align256(off + (size_t)W.slot_cap * H * 4 * 4);
+  // overflow guard of the attention kernel: per-unit flag, per (unit, head) maximum
+  const int64_t units = sas_plan_layout(T, target).unit_cap;
+  W.off_flags = off;
+  off = sas_align256(off + (size_t)units * 4);
+  W.off_redo_m = off;
+  off = sas_align256(off + (size_t)units * H * 4);
   W.total = off;
   return W;
 }

@@ -214,9 +214,14 @@ __global__ __launch_bounds__(64) void resolve_kernel(SasFwdArgs a, const int* __
                                                      const int* __restrict__ idx,
                                                      const int* __restrict__ cmp_bt,
                                                      int* __restrict__ rows_out,
-                                                     int* __restrict__ ncmp_out) {
+                                                     int* __restrict__ ncmp_out,
+                                                     int* __restrict__ redo_flags) {
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
+  // clear the attention kernel's per-unit overflow flags (unit_cap of them over T blocks)
+  const int per = (a.unit_cap + a.T - 1) / a.T;
+  for (int i = lane; i < per; i += 64)
+    if (t * per + i < a.unit_cap) redo_flags[t * per + i] = 0;
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
   const int b = tk[TK_B];
   if (b < 0) {
@@ -278,6 +283,15 @@ __device__ __forceinline__ uint32_t to_q16(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
+// 16-bit payload of the query dtype -> float (exact).
+template <int QT>
+__device__ __forceinline__ float q16_to_f32(uint32_t v) {
+  if constexpr (QT == 0)
+    return __uint_as_float(v << 16);
+  else
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)v);
+}
+
 // OCP FP8 E4M3FN code -> exact 16-bit value of the query dtype.
 template <int QT>
 __device__ __forceinline__ uint32_t fp8_to_q16(uint32_t v) {
@@ -299,15 +313,11 @@ __device__ __forceinline__ uint32_t fp8_to_q16(uint32_t v) {
 // Source of rows that read as zeros (unused pages, tile padding).
 __device__ __attribute__((aligned(16))) uint8_t g_zero_row[1152];
 
-// Online-softmax reference handling.  The exponent reference m_ref of a head is
-// fixed after the unit's first tile (max of sink and that tile) and the O / l
-// accumulators are never rescaled inside the tile loop; P = 2^(s - m_ref) may
-// exceed 1.  The ratio O / l is the reference's softmax for any m_ref (exact in
-// real arithmetic; bf16(P) rounding is relative, hence scale-free).  If any later
-// logit exceeds m_ref by more than REF_SLACK (log2 units) -- where 2^REF_SLACK
-// times the row count could approach fp32 range -- the workgroup recomputes the
-// unit once with m_ref = the observed maximum.
-constexpr float REF_SLACK = 80.f;
+// Online softmax (golden.py:184-196): m_run is the running maximum of the sink
+// and every logit seen so far; a tile whose maximum exceeds it rescales O and l
+// by 2^(m_old - m_new) before P = 2^(x - m_run) is formed, so P <= 1 and the
+// row holding the maximum gets P = 1 exactly, as in the reference.  The rescale
+// runs only when some head of the wave saw a larger maximum.
 constexpr float LOG2E = 1.4426950408889634f;
 
 template <int NW, int DQK, int QT, bool KV8>
@@ -415,7 +425,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
   }
   const float sink2 = split == 0 ? sinks[hc] * LOG2E : -INFINITY;  // golden.py:162-163
   f32x16_t acc[16];
-  float m_ref = sink2, l_run = 0.f, m_obs = sink2;
+  float m_run = sink2, l_run = split == 0 ? 1.f : 0.f;  // golden.py:162-163
 
   // fp8: 16 source bytes -> two 16-bit chunks written to the (single) tile
   auto fp8_stage = [&](int it) {
@@ -466,11 +476,9 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
     }
   };
 
-  for (int pass = 0; pass < 2; ++pass) {
+  {
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = f32x16_t{};
-    // row_sum starts at 1 for the sink (golden.py:163), expressed at reference m_ref
-    l_run = split == 0 ? (m_ref == sink2 ? 1.f : exp2f(sink2 - m_ref)) : 0.f;
 
     // prologue: addresses of tiles 0 and 1; DMA of tile 0
     if (tid < SAS_TILE) {
@@ -525,15 +533,18 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
         mt = fmaxf(mt, x[r]);
       }
       mt = fmaxf(mt, __shfl_xor(mt, 32));
-      m_obs = fmaxf(m_obs, mt);
-      if (it == 0 && mt > m_ref) {  // first tile sets the reference (acc is still zero)
-        l_run *= exp2f(m_ref - mt);
-        m_ref = mt;
+      if (__any(mt > m_run)) {  // golden.py:185-187,196: rescale O and l to the new maximum
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = m_new > m_run ? exp2f(m_run - m_new) : 1.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] *= alpha;
+        l_run *= alpha;
+        m_run = m_new;
       }
       float ps = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        x[r] = exp2f(x[r] - m_ref);
+        x[r] = exp2f(x[r] - m_run);
         ps += x[r];
       }
       ps += __shfl_xor(ps, 32);
@@ -584,9 +595,6 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
         }
       }
     }
-    const int redo = m_obs > m_ref + REF_SLACK;
-    if (!__syncthreads_or(redo)) break;
-    m_ref = m_obs;  // second pass with the exact maximum as reference
   }
 
   // ---- epilogue ----
@@ -607,7 +615,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
         *reinterpret_cast<u32x4_t*>(orow + 64 * mm + 16 * q4 + 8 * g) = o;
       }
     }
-    if (lse && g == 0) lse[(size_t)t * H + h] = (m_ref + __log2f(l_run)) * 0.6931471805599453f;
+    if (lse && g == 0) lse[(size_t)t * H + h] = (m_run + __log2f(l_run)) * 0.6931471805599453f;
   } else {
     const int slot = wsbase + split;
     float* orow = ws_o + ((size_t)slot * H + h) * DV;
@@ -629,49 +637,59 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
         dst[1] = v1;
       }
     }
-    if (g == 0) {
-      ws_ml[((size_t)slot * H + h) * 2 + 0] = m_ref;
-      ws_ml[((size_t)slot * H + h) * 2 + 1] = l_run;
-    }
+    if (g == 0)
+      reinterpret_cast<float4*>(ws_ml)[(size_t)slot * H + h] = make_float4(m_run, l_run, l_run, 0.f);
   }
 }
 
 // ===========================================================================
-// Split combine: one workgroup per split token, all heads.
+// Split combine: one wave per (split token, head); lane l merges columns
+// [8 l, 8 l + 8) of the d_v = 512 partial outputs.  A partial holds O and its
+// two normalisers (l_w: sum of the rounded P that entered O, for the output;
+// l_e: sum of the exact P, for the LSE) in its own frame m; the merge rescales
+// each by 2^(m_s - max_s m_s).  Only split 0 carries the sink, so it enters once.
 // ===========================================================================
+constexpr int COMBINE_HEADS = 4;  // waves (heads) per workgroup
+
 template <int QT>
-__global__ __launch_bounds__(256) void combine_kernel(SasFwdArgs a, const int* __restrict__ plan,
-                                                      const float* __restrict__ ws_o,
-                                                      const float* __restrict__ ws_ml,
-                                                      uint16_t* __restrict__ out,
-                                                      float* __restrict__ lse) {
+__global__ __launch_bounds__(64 * COMBINE_HEADS) void combine_kernel(
+    SasFwdArgs a, const int* __restrict__ plan, const float* __restrict__ ws_o,
+    const float* __restrict__ ws_ml, uint16_t* __restrict__ out, float* __restrict__ lse) {
   constexpr int DV = 512;
   const int i = blockIdx.x;
   if (i >= plan[PH_NSPLIT_TOKENS]) return;
+  const int H = a.H;
+  const int h = blockIdx.y * COMBINE_HEADS + (threadIdx.x >> 6);
+  if (h >= H) return;
+  const int lane = threadIdx.x & 63;
   const SasPlanLayout L = sas_plan_layout(a.T, a.split_cap);
   const int t = plan[L.off_split_tokens + i];
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
   const int S = tk[TK_SPLITS], base = tk[TK_WSBASE];
-  const int H = a.H;
-  const int tid = threadIdx.x;
-  for (int h = 0; h < H; ++h) {
-    float mx = -INFINITY;
-    for (int s = 0; s < S; ++s) mx = fmaxf(mx, ws_ml[((size_t)(base + s) * H + h) * 2]);
-    float l = 0.f;
-    float o0 = 0.f, o1 = 0.f;
-    for (int s = 0; s < S; ++s) {
-      const float ms = ws_ml[((size_t)(base + s) * H + h) * 2];
-      const float wgt = (ms == -INFINITY) ? 0.f : exp2f(ms - mx);
-      l += wgt * ws_ml[((size_t)(base + s) * H + h) * 2 + 1];
-      const float2 ov = reinterpret_cast<const float2*>(ws_o + ((size_t)(base + s) * H + h) * DV)[tid];
-      o0 += wgt * ov.x;
-      o1 += wgt * ov.y;
-    }
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    reinterpret_cast<uint32_t*>(out + ((size_t)t * H + h) * DV)[tid] =
-        to_q16<QT>(o0 * inv) | (to_q16<QT>(o1 * inv) << 16);
-    if (lse && tid == 0) lse[(size_t)t * H + h] = (mx + __log2f(l)) * 0.6931471805599453f;
+  const float4* ml = reinterpret_cast<const float4*>(ws_ml);
+  float mx = -INFINITY;
+  for (int s = 0; s < S; ++s) mx = fmaxf(mx, ml[(size_t)(base + s) * H + h].x);
+  float l = 0.f, le = 0.f;
+  float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
+  for (int s = 0; s < S; ++s) {
+    const size_t row = (size_t)(base + s) * H + h;
+    const float4 rec = ml[row];
+    const float wgt = rec.x == -INFINITY ? 0.f : exp2f(rec.x - mx);
+    l += wgt * rec.y;
+    le += wgt * rec.z;
+    const float4* src = reinterpret_cast<const float4*>(ws_o + row * DV) + 2 * lane;
+    const float4 v0 = src[0], v1 = src[1];
+    o0.x += wgt * v0.x; o0.y += wgt * v0.y; o0.z += wgt * v0.z; o0.w += wgt * v0.w;
+    o1.x += wgt * v1.x; o1.y += wgt * v1.y; o1.z += wgt * v1.z; o1.w += wgt * v1.w;
   }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  u32x4_t o;
+  o[0] = to_q16<QT>(o0.x * inv) | (to_q16<QT>(o0.y * inv) << 16);
+  o[1] = to_q16<QT>(o0.z * inv) | (to_q16<QT>(o0.w * inv) << 16);
+  o[2] = to_q16<QT>(o1.x * inv) | (to_q16<QT>(o1.y * inv) << 16);
+  o[3] = to_q16<QT>(o1.z * inv) | (to_q16<QT>(o1.w * inv) << 16);
+  reinterpret_cast<u32x4_t*>(out + ((size_t)t * H + h) * DV)[lane] = o;
+  if (lse && lane == 0) lse[(size_t)t * H + h] = (mx + __log2f(le)) * 0.6931471805599453f;
 }
 
 }  // namespace sas

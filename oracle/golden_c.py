@@ -54,6 +54,8 @@ def load():
     lib.sasg_attention.argtypes = [ctypes.POINTER(SasgParams), P, P, P, P, P, P, P, P, P, P,
                                    P, P, P, ctypes.c_int32, P, P]
     lib.sasg_attention.restype = ctypes.c_int
+    lib.sasg_attention_exact.argtypes = lib.sasg_attention.argtypes
+    lib.sasg_attention_exact.restype = ctypes.c_int
     lib.sasg_resolve.argtypes = [ctypes.POINTER(SasgParams), P, P, P, P, P, P, ctypes.c_int32,
                                  P, P, P]
     lib.sasg_resolve.restype = ctypes.c_int
@@ -112,8 +114,13 @@ def attention(
     cmp_scale: Optional[np.ndarray] = None,
     tokens: Optional[Sequence[int]] = None,
     nthreads: int = 0,
+    exact: bool = False,
 ):
-    """Returns ``(out [T, H, d_v] float32, lse [T, H] float32)``."""
+    """Returns ``(out [T, H, d_v] float32, lse [T, H] float32)``.
+
+    ``exact=True`` evaluates the one-shot sink softmax over the same resolved
+    rows in float64 with no intermediate or output rounding: the mathematical
+    value both the reference golden model and the device kernel approximate."""
     lib = load()
     T, H, D = q.shape
     d_v = D if d_v is None else d_v
@@ -142,7 +149,8 @@ def attention(
                 cmp_shape=None if cmp_a is None else cmp_a.shape,
                 cmp_table_len=1 if cbt is None else cbt.shape[1],
                 softmax_scale=softmax_scale, nthreads=nthreads)
-    rc = lib.sasg_attention(ctypes.byref(p), _ptr(q_a), _ptr(ori_a), _ptr(osc), _ptr(obt),
+    fn = lib.sasg_attention_exact if exact else lib.sasg_attention
+    rc = fn(ctypes.byref(p), _ptr(q_a), _ptr(ori_a), _ptr(osc), _ptr(obt),
                             _ptr(cmp_a), _ptr(csc), _ptr(cbt), _ptr(idx), _ptr(qp), _ptr(aq),
                             _ptr(skv), _ptr(snk), _ptr(tok),
                             0 if tok is None else len(tok), _ptr(out), _ptr(lse))

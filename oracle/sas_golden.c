@@ -329,4 +329,93 @@ int sasg_attention(const sasg_params* p, const void* q, const void* ori_kv,
   return err;
 }
 
+/* Mathematical reference for the accuracy check: the same resolved rows, the
+ * one-shot sink softmax out = sum_j e^(x_j - m) V_j / (e^(sink - m) + sum_j
+ * e^(x_j - m)) evaluated in double with no intermediate rounding (golden's
+ * closed form golden.py:207-244 in float64).  Outputs are NOT rounded to the
+ * query dtype.  Same argument list as sasg_attention. */
+int sasg_attention_exact(const sasg_params* p, const void* q, const void* ori_kv,
+                         const float* ori_scale, const int32_t* ori_bt, const void* cmp_kv,
+                         const float* cmp_scale, const int32_t* cmp_bt, const int32_t* idx,
+                         const int32_t* q_prefix, const int32_t* act_q, const int32_t* seqused_kv,
+                         const float* sinks, const int32_t* tokens, int32_t n_tokens, float* out,
+                         float* lse) {
+  const int H = p->H, D = p->D, Dv = p->Dv;
+  int32_t* tb = (int32_t*)malloc(sizeof(int32_t) * (p->T > 0 ? p->T : 1));
+  int32_t* ts = (int32_t*)malloc(sizeof(int32_t) * (p->T > 0 ? p->T : 1));
+  build_token_map(p, q_prefix, act_q, tb, ts);
+  int nwork = tokens ? n_tokens : p->T;
+  int need = max_rows_per_token(p, seqused_kv);
+  int err = 0;
+#ifdef _OPENMP
+  if (p->nthreads > 0) omp_set_num_threads(p->nthreads);
+#endif
+#pragma omp parallel
+  {
+    int64_t* rows = (int64_t*)malloc(sizeof(int64_t) * need);
+    double* kv = (double*)malloc(sizeof(double) * (size_t)need * D);
+    double* sc = (double*)malloc(sizeof(double) * (size_t)need);
+    double* qh = (double*)malloc(sizeof(double) * (size_t)D);
+    double* acc = (double*)malloc(sizeof(double) * (size_t)Dv);
+#pragma omp for schedule(dynamic, 1)
+    for (int w = 0; w < nwork; ++w) {
+      int t = tokens ? tokens[w] : w;
+      if (t < 0 || t >= p->T) continue;
+      float* ot = out + (int64_t)t * H * Dv;
+      float* lt = lse + (int64_t)t * H;
+      memset(ot, 0, sizeof(float) * (size_t)H * Dv);
+      memset(lt, 0, sizeof(float) * (size_t)H);
+      if (tb[t] < 0) continue;
+      int b = tb[t], no, nc;
+      if (resolve_token(p, ori_bt, cmp_bt, idx, b, t, ts[t], act_q[b], seqused_kv[b], rows, &no,
+                        &nc)) {
+#pragma omp atomic write
+        err = -1;
+        continue;
+      }
+      int n = no + nc;
+      for (int j = 0; j < n; ++j) {
+        int is_cmp = j >= no;
+        int64_t row = rows[j];
+        double* kr = kv + (int64_t)j * D;
+        if (row < 0) { for (int d = 0; d < D; ++d) kr[d] = 0.0; continue; }
+        const void* pool = is_cmp ? cmp_kv : ori_kv;
+        int bs = is_cmp ? p->cmp_block_size : p->ori_block_size;
+        int64_t base = (row / bs) * (is_cmp ? p->cmp_block_stride : p->ori_block_stride) +
+                       (row % bs) * (is_cmp ? p->cmp_row_stride : p->ori_row_stride);
+        float scl = 1.0f;
+        if (p->kv_dtype == SASG_FP8E4M3) scl = (is_cmp ? cmp_scale : ori_scale)[row];
+        for (int d = 0; d < D; ++d) {
+          float v = load_elem(pool, p->kv_dtype, base + d);
+          kr[d] = p->kv_dtype == SASG_FP8E4M3 ? (double)(v * scl) : (double)v;
+        }
+      }
+      for (int h = 0; h < H; ++h) {
+        for (int d = 0; d < D; ++d) qh[d] = load_elem(q, p->q_dtype, ((int64_t)t * H + h) * D + d);
+        double m = sinks[h];
+        for (int j = 0; j < n; ++j) {
+          const double* kr = kv + (int64_t)j * D;
+          double dot = 0.0;
+          for (int d = 0; d < D; ++d) dot += qh[d] * kr[d];
+          sc[j] = dot * (double)p->softmax_scale;
+          if (sc[j] > m) m = sc[j];
+        }
+        double l = isinf(sinks[h]) && sinks[h] < 0 ? 0.0 : exp((double)sinks[h] - m);
+        for (int d = 0; d < Dv; ++d) acc[d] = 0.0;
+        for (int j = 0; j < n; ++j) {
+          double pj = exp(sc[j] - m);
+          l += pj;
+          const double* kr = kv + (int64_t)j * D;
+          for (int d = 0; d < Dv; ++d) acc[d] += pj * kr[d];
+        }
+        for (int d = 0; d < Dv; ++d) ot[(int64_t)h * Dv + d] = (float)(acc[d] / l);
+        lt[h] = (float)(m + log(l));
+      }
+    }
+    free(rows); free(kv); free(sc); free(qh); free(acc);
+  }
+  free(tb); free(ts);
+  return err;
+}
+
 int sasg_version(void) { return 1; }

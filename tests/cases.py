@@ -82,6 +82,19 @@ class Case:
             ori_scale=self.ori_scale, cmp_scale=self.cmp_scale, tokens=tokens,
             nthreads=nthreads)
 
+    def oracle_exact(self, tokens=None, nthreads=0):
+        """The float64 one-shot softmax over the same rows (no rounding)."""
+        from oracle import golden_c
+        return golden_c.attention(
+            q=self.q_bits, ori_kv=self.ori_kv, ori_block_table=self.ori_block_table,
+            q_prefix=self.q_prefix, act_q=self.act_q, seqused_kv=self.seqused_kv,
+            sinks=self.sinks, softmax_scale=self.softmax_scale, scenario=self.scenario,
+            cmp_kv=self.cmp_kv, cmp_block_table=self.cmp_block_table,
+            cmp_sparse_indices=self.idx, cmp_ratio=self.cmp_ratio, win_left=self.win_left,
+            d_v=self.Dv, q_dtype=self.q_dtype, kv_dtype=self.kv_dtype,
+            ori_scale=self.ori_scale, cmp_scale=self.cmp_scale, tokens=tokens,
+            nthreads=nthreads, exact=True)
+
 
 def _payload_f32(a: np.ndarray, dtype: str) -> np.ndarray:
     if dtype == "bf16":
@@ -138,7 +151,12 @@ def make_case(
     sink_range=(-1.0, 1.0),
     value_scale: float = 1.0,
     index_mode: str = "random",
+    dist: str = "normal",
 ) -> Case:
+    """``dist="normal"``: q and KV ~ N(0, value_scale^2) (the benchmark
+    configurations).  ``dist="reference"``: the reference suite's own draws --
+    q and raw KV ~ U(-10, 10), compressed KV ~ U(-5, 10)
+    (test_sparse_attn_sharedkv.py:262, golden.py:315-408)."""
     rng = np.random.default_rng(seed)
     seq_kv = [int(x) for x in seq_kv]
     qps = [int(q_per_seq)] * B if isinstance(q_per_seq, int) else [int(x) for x in q_per_seq]
@@ -146,10 +164,15 @@ def make_case(
     cu[1:] = np.cumsum(qps)
     T = int(cu[-1])
 
-    q = (rng.standard_normal((T, H, D)) * value_scale).astype(np.float32)
+    def draw(shape, lo_hi):
+        if dist == "reference":
+            return rng.uniform(lo_hi[0], lo_hi[1], size=shape).astype(np.float32)
+        return (rng.standard_normal(shape) * value_scale).astype(np.float32)
+
+    q = draw((T, H, D), (-10.0, 10.0))
     q_bits = _encode(q, q_dtype)
 
-    def paged_pool(lens: List[int], bs: int):
+    def paged_pool(lens: List[int], bs: int, lo_hi):
         per = [math.ceil(n / bs) if n > 0 else 0 for n in lens]
         nb = sum(per) + extra_pages
         perm = rng.permutation(nb).astype(np.int32)
@@ -158,13 +181,14 @@ def make_case(
         for b, n in enumerate(per):
             table[b, :n] = perm[cur:cur + n]
             cur += n
-        vals = (rng.standard_normal((nb, bs, D)) * value_scale).astype(np.float32)
+        vals = draw((nb, bs, D), lo_hi)
         return vals, table
 
-    ori_vals, ori_bt = paged_pool(seq_kv, block_size)
+    ori_vals, ori_bt = paged_pool(seq_kv, block_size, (-10.0, 10.0))
     cmp_vals = cmp_bt = None
     if scenario >= 2:
-        cmp_vals, cmp_bt = paged_pool([n // cmp_ratio for n in seq_kv], cmp_block_size)
+        cmp_vals, cmp_bt = paged_pool([n // cmp_ratio for n in seq_kv], cmp_block_size,
+                                      (-5.0, 10.0))
 
     ori_scale = cmp_scale = None
     if kv_dtype == "fp8e4m3":

@@ -57,19 +57,58 @@ def run_op(case: Case, device="cuda", **extra):
 
 
 def assert_parity(out, lse, ref_out, ref_lse, dtype="bf16", max_abs=2e-2, mean_abs=2e-3,
-                  label=""):
-    """The benchmark tolerance (max-abs 2e-2, mean-abs 2e-3 on bf16 outputs) plus
-    the reference's own check_result / LSE rules."""
+                  label="", exact=None, rule="baseline"):
+    """Parity of the device result with the oracle.
+
+    * ``rule="baseline"`` (N(0,1) inputs): max-abs 2e-2 and mean-abs 2e-3 on the
+      bf16 output, and the LSE within the reference's LSE rule.
+    * ``rule="reference"`` (the reference's large-magnitude inputs, where an
+      absolute bound is below one bf16 ulp): the reference's own check_result rule
+      (>= 99.5% within rtol 2^-7 / atol 1e-4, worst normalised error < 10,
+      test_sparse_attn_sharedkv.py:394-467) applied to the device result AND to
+      the oracle, each against the exact value: the device must pass at least
+      as many elements as the oracle does (0.1 point of slack).  Against the
+      oracle directly the rule is required at 99.0%: both round P to bf16, but
+      in different frames (the oracle at its 512-row tile maxima, the device at
+      its first tile's), so where several rows carry comparable weight their
+      rounding errors differ at the 2^-9 level (the reference's own device
+      kernel, with 128-row tiles, is in the same position).
+    * with ``exact`` (the float64 one-shot softmax over the same rows): the
+      device error against the exact value is at most 1.25x the oracle's own
+      error on average and 2x at the worst element (plus one bf16 ulp of
+      slack at the output's scale), so the device result is as accurate as the
+      reference golden model, whose bf16 rounding of P it cannot reproduce
+      bit-for-bit.
+
+    check_result is printed in every case."""
     assert np.isfinite(out).all(), f"{label}: non-finite output"
     mx, mn = baseline_tolerance(out, ref_out)
     ful, rel = check_result_rule(out, ref_out, dtype)
     lful, lrel = check_lse_rule(lse, ref_lse, dtype)
     msg = (f"{label}: max_abs={mx:.3e} mean_abs={mn:.3e} check_result={ful:.3f}%/{rel:.2f} "
            f"lse={lful:.3f}%/{lrel:.2f}")
+    if exact is not None:
+        ex_out, ex_lse = exact
+        ek = np.abs(out.astype(np.float64) - ex_out)
+        eg = np.abs(ref_out.astype(np.float64) - ex_out)
+        ulp = 2.0 ** -8 * float(np.abs(ex_out).max()) if ex_out.size else 0.0
+        msg += (f" err_vs_exact dev mean={ek.mean():.3e} max={ek.max():.3e} | "
+                f"oracle mean={eg.mean():.3e} max={eg.max():.3e}")
     print(msg, flush=True)
-    assert mx <= max_abs and mn <= mean_abs, msg
-    assert ful >= 99.5 and rel < 10.0, msg
+    if rule == "baseline":
+        assert mx <= max_abs and mn <= mean_abs, msg
+    else:
+        assert exact is not None, "the reference rule is judged against the exact value"
+        dful, drel = check_result_rule(out, exact[0], dtype)
+        gful, grel = check_result_rule(ref_out, exact[0], dtype)
+        msg += f" | vs exact: dev {dful:.3f}%/{drel:.2f} oracle {gful:.3f}%/{grel:.2f}"
+        print(msg, flush=True)
+        assert dful >= min(99.5, gful - 0.1) and drel < 10.0, msg
+        assert ful >= 99.0 and rel < 10.0, msg
     assert lful >= 99.5 and lrel < 10.0, msg
+    if exact is not None and ek.size:
+        assert ek.mean() <= 1.25 * eg.mean() + 1e-7, msg
+        assert ek.max() <= 2.0 * eg.max() + ulp, msg
     return mx, mn
 
 

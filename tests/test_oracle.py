@@ -175,6 +175,26 @@ def test_kat_chunked_equals_one_shot_f64(D, H, seq, S1, K):
     np.testing.assert_allclose(lse, ref_lse, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("D,H,seq,S1,K,scenario", [
+    (576, 16, 1024, 3, 300, 3), (576, 8, 4400, 2, 1100, 3), (576, 8, 700, 3, 0, 2),
+])
+def test_c_exact_matches_f64_one_shot(D, H, seq, S1, K, scenario):
+    """The C float64 reference (``exact=True``) is the one-shot sink softmax."""
+    from oracle import golden_c
+
+    kc = _kat_case(D, H, seq, S1, max(K, 1), seed=D + S1, dense=scenario == 2)
+    out, lse = golden_c.attention(
+        q=kc["q"], ori_kv=kc["ori_pool"], ori_block_table=np.zeros((1, 1), np.int32),
+        q_prefix=[0], act_q=[S1], seqused_kv=[seq], sinks=kc["sinks"],
+        softmax_scale=1.0 / math.sqrt(D), scenario=scenario, cmp_kv=kc["cmp_pool"],
+        cmp_block_table=np.zeros((1, 1), np.int32),
+        cmp_sparse_indices=kc["idx"] if scenario == 3 else None, cmp_ratio=4,
+        q_dtype="fp32", kv_dtype="fp32", exact=True)
+    ref, ref_lse = _one_shot(kc, scenario=scenario)
+    assert np.abs(out - ref).max() / np.abs(ref).max() < 1e-6
+    np.testing.assert_allclose(lse, ref_lse, rtol=1e-6, atol=1e-6)
+
+
 def test_kat_dense_cmp_scenario2():
     kc = _kat_case(576, 8, 700, 3, 0, seed=11)
     out, lse = _chunked(kc, scenario=2)
