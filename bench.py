@@ -278,6 +278,33 @@ def cpu_baseline(name, n_seq, seed=0):
                 sample=f"{sample}; sample took {secs:.2f} s")
 
 
+def profile_attend(name, steps, dev, core_num=256):
+    """Plan and resolve once, then launch only the attention stage `steps` times
+    (the kernel the roofline rates), for rocprofv3 counter runs."""
+    from dsv4_planb_amd import metadata as M
+    from dsv4_planb_amd.api import build_launch
+
+    wl = make_workload(name, seed=0, dev=dev)
+    cu = wl["cu"]
+    plan = M.sparse_attn_sharedkv_metadata(
+        num_heads_q=wl["H"], num_heads_kv=1, head_dim=D_QK, cu_seqlens_q=cu,
+        seqused_kv=wl["seqused"], batch_size=wl["B"], max_seqlen_q=wl["q_per"],
+        max_seqlen_kv=max(wl["kv"]), cmp_topk=wl["K"], cmp_ratio=RATIO, layout_q="TND",
+        has_cmp_kv=True, aic_core_num=core_num)
+    launch, out, lse = build_launch(
+        q_flat=wl["q"], ori_kv=wl["ori_kv"], ori_block_table=wl["ori_bt"], cmp_kv=wl["cmp_kv"],
+        cmp_block_table=wl["cmp_bt"], cmp_indices=wl["idx"], q_prefix=cu[:-1],
+        act_q_lens=cu[1:] - cu[:-1], seqused_kv=wl["seqused"], sinks=wl["sinks"],
+        metadata=plan, scenario=3, topk=wl["K"], cmp_ratio=RATIO, ori_win_left=WIN - 1,
+        softmax_scale=1.0 / math.sqrt(D_QK), core_num=core_num)
+    launch.run("resolve")
+    for _ in range(steps):
+        launch.run("attend")
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "attend", "workload": name, "launches": steps,
+                      "alg_bytes": wl["alg_bytes"], "alg_flops": wl["alg_flops"]}))
+
+
 def main_r_batch(name):
     return dict(decode128k=128, decode32=32, prefill8k=1)[name]
 
@@ -295,6 +322,10 @@ def main():
     ap.add_argument("--cpu-seqs", type=int, default=0,
                     help="cap on sampled sequences for the CPU baseline (0 = size for ~10 s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mode", default="bench", choices=["bench", "attend", "copy"],
+                    help="bench: the JSON line; attend: only the attention stage of --workload, "
+                         "--steps launches (for counter runs); copy: a 1 GiB device copy, "
+                         "--steps times (calibrates the HBM byte counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -306,6 +337,17 @@ def main():
 
     torch.backends.cuda.matmul.allow_tf32 = False
     dev = torch.device("cuda:0")
+    if args.mode == "copy":
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "copy", "bytes_per_copy": src.numel(), "copies": args.steps}))
+        return
+    if args.mode == "attend":
+        profile_attend(args.workload, args.steps, dev)
+        return
     results = {}
     for name in [args.workload] + [w for w in args.extra.split(",") if w and w != args.workload]:
         _log(f"{name}: building inputs")

@@ -164,7 +164,9 @@ def build_launch(
     if scenario == 3:
         idx = _dev_i32(cmp_indices, dev).reshape(T, -1)
         keep.append(idx)
-    p.topk = topk if scenario == 3 else 0
+    # scenario 3: index slots per token; scenario 2: capacity of the per-token list
+    # of causally valid compressed rows -- the rows the block table covers
+    p.topk = topk if scenario == 3 else (p.cmp_table_len * p.cmp_block_size if scenario == 2 else 0)
     p.cmp_ratio = cmp_ratio
     p.scenario = scenario
     p.ori_win_left = ori_win_left

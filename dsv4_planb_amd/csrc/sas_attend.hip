@@ -5,16 +5,14 @@
 // its compressed rows).  Wave w owns query heads [32 w, 32 w + 32); Q stays in
 // VGPRs (36 x 16-B fragments at d_qk = 576) and the fp32 O^T accumulator of
 // 512 x 32 fills the AGPRs.  KV rows are gathered 32 at a time (one tile) by
-// direct global -> LDS DMA (16 B per lane) into a 4-slot ring, so two tiles are
-// in flight while one is consumed and the one before it finishes its PV.
+// direct global -> LDS DMA (16 B per lane) into a 4-slot ring, three tiles ahead
+// of the one being consumed.
 //
 // Per tile, per wave (32 keys x 32 heads):
 //   S^T = K Q^T      36 MFMA 32x32x16, A = K rows from LDS (ds_read_b128), B = Q
 //   softmax          P = 2^(x - m) in a per-unit frame m, bf16(P)
 //   O^T += V^T P^T   32 MFMA, A = V^T read transposed from LDS (ds_read_b64_tr_b16),
 //                    B = P^T straight from the S^T accumulator registers
-// The PV of tile i-1 is issued in the same basic block as the softmax of tile i
-// so the MFMA pipe has independent work while the VALU computes exponentials.
 //
 // Softmax (reference golden.py:156-200): the state of a head is (m, l, O) seeded
 // with (sink, 1, 0) on the unit that holds the token's first rows.  O / l and
@@ -25,9 +23,10 @@
 // bf16-rounded P that enter PV, so O / l_w is exactly a convex combination of
 // the V rows (a one-hot softmax returns its row unchanged, as the reference's
 // P = 1 does); l_e sums the unrounded P and gives the LSE.  A logit more than
-// REDO_SLACK above the frame flags the unit; the redo pass (attend_redo_kernel,
-// always launched after the first pass, about one workgroup per CU striding over
-// the flags) recomputes flagged units framed on the maximum the first pass saw.
+// REDO_SLACK above the frame (where 2^SLACK times the row count nears the fp32
+// range) makes the workgroup discard the pass and recompute the unit framed on
+// the maximum each head observed (a second, separately inlined copy of the unit
+// body, so the common path carries no extra live state).
 //
 // LDS tile = latent region (32 rows x 512 dims at a 1088-B row stride, i.e. 64 B
 // of padding per row) + rope region (32 rows x 64 dims, 128-B rows; absent at
@@ -95,18 +94,21 @@ struct AttendLds {
   static constexpr int TILEB = SAS_TILE * (1024 + 64) + SAS_TILE * (DQK - 512) * 2;
   uint8_t tiles[4 * TILEB];
   const uint8_t* rowaddr[4][SAS_TILE];
+  int codes[4][SAS_TILE];  // row codes of the next tiles, fetched by DMA
+  int far;                 // a logit of some head outgrew the frame
 };
 
-// One work unit u.  REDO: the unit was flagged by the first pass; recompute it in
-// the frame of the maximum that pass observed.
+// One work unit u.  Returns true (workgroup-uniform) when the first pass must be
+// redone; m_obs then holds each lane's observed maximum (log2 units), which the
+// REDO instance takes as its frame.
 template <int DQK, int QT, bool REDO>
-__device__ __forceinline__ void attend_unit(
+__device__ __forceinline__ bool attend_unit(
     int u, AttendLds<DQK>& sm, const SasFwdArgs& a, const uint16_t* __restrict__ q,
     const uint8_t* __restrict__ ori_kv, const uint8_t* __restrict__ cmp_kv,
     const int* __restrict__ cmp_bt, const int* __restrict__ rows_list,
     const int* __restrict__ ncmp, const float* __restrict__ sinks, const int* __restrict__ plan,
     uint16_t* __restrict__ out, float* __restrict__ lse, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, int* __restrict__ redo_flags, float* __restrict__ redo_m) {
+    float* __restrict__ ws_ml, float& m_obs) {
   constexpr int DV = 512;
   constexpr int NT = 256;
   constexpr int TILE = SAS_TILE;          // 32 keys
@@ -141,7 +143,7 @@ __device__ __forceinline__ void attend_unit(
       reinterpret_cast<u32x4_t*>(out + (size_t)t * H * DV)[i] = u32x4_t{0, 0, 0, 0};
     if (lse)
       for (int i = tid; i < H; i += NT) lse[(size_t)t * H + i] = 0.f;
-    return;
+    return false;
   }
 
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
@@ -152,16 +154,9 @@ __device__ __forceinline__ void attend_unit(
   const int ntiles = r1 > r0 ? (r1 - r0 + TILE - 1) / TILE : 0;
   const int* codes = rows_list + (size_t)t * a.list_stride;
 
-  // Row code of list row r (-1 = a row read as zeros): window rows first, then
-  // compressed rows (resolved list in scenario 3, every row below thr in 2).
-  auto row_code = [&](int r) -> int {
-    if (r >= r1) return -1;
-    if (r < nwin) return codes[r];
-    const int j = r - nwin;
-    if (a.scenario == 3) return codes[a.win_left + 1 + j];
-    return paged_code(cmp_bt + (size_t)b * a.cmp_table_len, a.cmp_table_len, a.cmp_block_size,
-                      a.cmp_block_num, j);
-  };
+  // Row code of list row r (-1 = a row read as zeros): the token's list holds its
+  // window rows, then its compressed rows, contiguously.
+  auto row_code = [&](int r) -> int { return r < r1 ? codes[r] : -1; };
   auto row_ptr = [&](int r, int code) -> const uint8_t* {
     if (code < 0) return g_zero_row;
     if (r < nwin) {
@@ -219,41 +214,64 @@ __device__ __forceinline__ void attend_unit(
   for (int i = 0; i < 16; ++i) acc[i] = f32x16_t{};
   // golden.py:162-163: the unit holding the token's first rows carries the sink
   const float sink2 = split == 0 ? sinks[hc] * LOG2E : -INFINITY;
-  float m_run = sink2;
-  if (REDO) m_run = redo_m[(size_t)u * H + hc];  // frame = the maximum the first pass saw
+  float m_run = REDO ? m_obs : sink2;  // redo: the frame is the maximum pass 1 observed
 
   // ---- gather: tile i goes to ring slot i & 3 ----
   // Latent: instruction k of wave w copies row 4 k + w; lane l fetches source chunk
   // l ^ swz_a(4 k + w) = l ^ (k & 3) into slot l.  Rope: wave w copies rows
   // 8 w .. 8 w + 7, lane l row 8 w + (l >> 3), slot l & 7 <- chunk (l & 7) ^ swz_b(row).
+  const int wu = __builtin_amdgcn_readfirstlane(w);  // the wave index as a scalar
+  const uint32_t ulane = (uint32_t)lane;
   auto dma_tile = [&](int i) {
     const int slot = i & (NSTAGE - 1);
     lds_u8* dstA = tiles + slot * TILEB;
-    const uint64_t mine = (uint64_t)rowaddr[slot][4 * (lane & 7) + w];
+    const uint64_t mine = (uint64_t)rowaddr[slot][4 * (lane & 7) + wu];
 #pragma unroll
     for (int k = 0; k < TILE / 4; ++k) {
       const uint64_t rb = ((uint64_t)__builtin_amdgcn_readlane((uint32_t)(mine >> 32), k) << 32) |
                           (uint32_t)__builtin_amdgcn_readlane((uint32_t)mine, k);
-      dma16((const uint8_t*)rb + 16 * (lane ^ (k & 3)), dstA + (4 * k + w) * STRA);
+      const uint32_t off = 16u * (ulane ^ (uint32_t)(k & 3));
+      dma16((const uint8_t*)rb + off, dstA + (4 * k + wu) * STRA);
     }
     if constexpr (ROPE) {
-      const int row = 8 * w + (lane >> 3);
+      const int row = 8 * wu + (lane >> 3);
       const uint8_t* rr = rowaddr[slot][row];
-      dma16(rr + ROWA + 16 * ((lane & 7) ^ swz_b(row)), dstA + TILEA + 8 * w * ROWR);
+      dma16(rr + (uint32_t)(ROWA + 16 * ((lane & 7) ^ swz_b(row))), dstA + TILEA + 8 * wu * ROWR);
     }
   };
 
-  // prologue: row addresses of tiles 0..2, DMA of tiles 0 and 1
+  // Row codes of tile i reach LDS by a 4-byte DMA (wave 0, lanes < 32, slot i & 3)
+  // so that no global load with a VGPR result sits inside the tile loop: the
+  // compiler would have to drain every outstanding tile DMA to consume it.
+  auto dma_codes = [&](int i) {
+    const int r = r0 + i * TILE + lane;
+    if (lane < TILE && r < r1)
+      __builtin_amdgcn_global_load_lds((const void*)(codes + r),
+                                       (__attribute__((address_space(3))) void*)&sm.codes[i & 3][0],
+                                       4, 0, 0);
+  };
+
+  // Pipeline, per iteration it (one barrier):
+  //   wait   until tile it has landed (tiles it+1, it+2 may still be in flight)
+  //   wave 0 writes the row addresses of tile it+3 (codes DMA'd two iterations ago)
+  //   barrier: tile it visible; every wave is done with tile it-1, whose slot
+  //            (= slot of it+3) is free
+  //   DMA    codes of tile it+5 (wave 0), then tile it+3 (all waves)
+  //   compute S, softmax and PV of tile it
+  // prologue: row addresses of tiles 0..2, codes of tiles 3 and 4, DMA of tiles 0..2
+  if (!REDO && tid == 0) sm.far = 0;
   if (tid < 3 * TILE) {
     const int r = r0 + tid;  // tile tid / 32, row tid % 32
     rowaddr[tid / TILE][tid % TILE] = row_ptr(r, row_code(r));
   }
   lds_barrier();
+  if (wu == 0) {
+    if (ntiles > 3) dma_codes(3);
+    if (ntiles > 4) dma_codes(4);
+  }
   if (ntiles > 0) dma_tile(0);
   if (ntiles > 1) dma_tile(1);
-
-  u32x4_t pk_prev[2];
-  const lds_u8* tile_prev = tiles;
+  if (ntiles > 2) dma_tile(2);
 
   // O^T += V^T P^T for one tile
   auto pv = [&](const lds_u8* tl, const u32x4_t(&pk)[2]) {
@@ -278,24 +296,30 @@ __device__ __forceinline__ void attend_unit(
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
   };
 
-  float l_w = split == 0 ? 1.f : 0.f, l_e = l_w;
-  if (REDO) {
-    const float alpha = split == 0 ? exp2f(sink2 - m_run) : 0.f;
-    l_w *= alpha;
-    l_e *= alpha;
-  }
-  float m_obs = m_run;
+  // Per-lane partial sums over this lane's keys (the two half-waves of a head see
+  // different keys); they are combined once, after the loop.
+  float pe = 0.f;          // sum of P (LSE)
+  float pw = 0.f;          // sum of bf16(P): what entered PV (output normaliser)
+  float xobs = -INFINITY;  // max of x - m over the unit, for the overflow guard
+  const float c = a.scale_log2;
   for (int it = 0; it < ntiles; ++it) {
-    // tile it has landed (this wave's share); at most tile it+1's DMA may be pending
-    if (it + 1 < ntiles)
+    // tile it has landed (this wave's share): the tile DMAs issued after it (at most
+    // two) may still be pending; wave 0's code DMAs were issued before those, so
+    // the same count also completes the codes of tile it+3
+    if (it + 2 < ntiles)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * CPT) : "memory");
+    else if (it + 1 < ntiles)
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CPT) : "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    lds_barrier();  // tile it visible to all waves; slot of tile it-2 is free
-    const int r3 = r0 + (it + 3) * TILE + lane;
-    int code3 = -1;
-    if (w == 0 && lane < TILE && it + 3 < ntiles) code3 = row_code(r3);  // before the DMA
-    if (it + 2 < ntiles) dma_tile(it + 2);
+    if (wu == 0 && it + 3 < ntiles && lane < TILE) {
+      const int r3 = r0 + (it + 3) * TILE + lane;
+      rowaddr[(it + 3) & (NSTAGE - 1)][lane] =
+          row_ptr(r3, r3 < r1 ? sm.codes[(it + 3) & 3][lane] : -1);
+    }
+    lds_barrier();
+    if (wu == 0 && it + 5 < ntiles) dma_codes(it + 5);  // before the tile DMA (vmcnt order)
+    if (it + 3 < ntiles) dma_tile(it + 3);
 
     const lds_u8* tl = tiles + (it & (NSTAGE - 1)) * TILEB;
     // ---- S^T = K Q^T (each K fragment is read one MFMA ahead) ----
@@ -318,74 +342,69 @@ __device__ __forceinline__ void attend_unit(
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read, one ahead
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (w == 0 && lane < TILE && it + 3 < ntiles)
-      rowaddr[(it + 3) & (NSTAGE - 1)][lane] = row_ptr(r3, code3);
 
-    // ---- softmax of tile it, overlapped with the PV of tile it-1 ----
+    // ---- softmax ----
+    // x = S c - m (log2 units); the first tile of the first pass fixes the frame m.
+    const bool first = !REDO && it == 0;
     float x[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] = s[r] * a.scale_log2;
+    for (int r = 0; r < 16; ++r) x[r] = first ? s[r] * c : fmaf(s[r], c, -m_run);
     const int nvalid = r1 - (r0 + it * TILE);
-    if (nvalid < TILE) {  // the unit's last tile: rows past r1 do not exist
+    if (__builtin_expect(nvalid < TILE, 0)) {  // the unit's last tile: rows past r1
       const int lim = nvalid - 4 * g;
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (8 * (r >> 2) + (r & 3) >= lim) x[r] = -INFINITY;
     }
-    float mt = x[0];
+    if (first) {  // O is still zero: no rescale needed
+      float mt = x[0];
 #pragma unroll
-    for (int r = 1; r < 16; ++r) mt = fmaxf(mt, x[r]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    m_obs = fmaxf(m_obs, mt);
-    if (!REDO && it == 0) {  // the first tile fixes the frame (O is still zero)
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = m_new > m_run ? exp2f(m_run - m_new) : 1.f;
-      l_w *= alpha;
-      l_e *= alpha;
-      m_run = m_new;
+      for (int r = 1; r < 16; ++r) mt = fmaxf(mt, x[r]);
+      m_run = fmaxf(m_run, fmaxf(mt, __shfl_xor(mt, 32)));
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] -= m_run;
     }
-    if (it > 0) pv(tile_prev, pk_prev);
-    float pe = 0.f, pw = 0.f;
+    float xm = x[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) xm = fmaxf(xm, x[r]);
+    xobs = fmaxf(xobs, xm);
     u32x4_t pk[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      x[r] = exp2f(x[r] - m_run);
+      x[r] = __builtin_amdgcn_exp2f(x[r]);  // 2^x; below 2^-126 of the frame flushes to 0
       pe += x[r];
     }
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t lo = to_q16<QT>(x[8 * kk + 2 * e]);
-        const uint32_t hi = to_q16<QT>(x[8 * kk + 2 * e + 1]);
-        pk[kk][e] = lo | (hi << 16);
-        pw += q16_to_f32<QT>(lo) + q16_to_f32<QT>(hi);
+        pk[kk][e] = pack2_q16<QT>(x[8 * kk + 2 * e], x[8 * kk + 2 * e + 1]);
+        pw = sum2_q16<QT>(pk[kk][e], pw);
       }
-    pe += __shfl_xor(pe, 32);
-    pw += __shfl_xor(pw, 32);
-    l_e += pe;
-    l_w += pw;
-    pk_prev[0] = pk[0];
-    pk_prev[1] = pk[1];
-    tile_prev = tl;
+    // ---- O^T += V^T P^T ----
+    pv(tl, pk);
   }
-  if (ntiles > 0) pv(tile_prev, pk_prev);
+  pe += __shfl_xor(pe, 32);
+  pw += __shfl_xor(pw, 32);
+  xobs = fmaxf(xobs, __shfl_xor(xobs, 32));
+  // golden.py:162-163: the sink seeds (m, l) = (sink, 1) on the token's first unit
+  const float l_sink = split != 0 ? 0.f : (sink2 == m_run ? 1.f : exp2f(sink2 - m_run));
+  const float l_e = l_sink + pe, l_w = l_sink + pw;
 
-  // ---- overflow guard: a logit far above the frame sends the unit to the redo pass ----
-  // Every wave records its observed maxima (clamped lanes write their head's own
-  // value), so a unit flagged by any wave is recomputed whole in consistent frames.
+  // ---- overflow guard: a logit far above the frame redoes the whole unit ----
   if (!REDO) {
-    redo_m[(size_t)u * H + hc] = m_obs;
-    if (__any(m_obs > m_run + REDO_SLACK)) {
-      if (lane == 0) redo_flags[u] = 1;
-      return;
+    if (__any(xobs > REDO_SLACK) && lane == 0) atomicOr(&sm.far, 1);
+    lds_barrier();
+    if (sm.far) {
+      m_obs = m_run + xobs;
+      return true;
     }
   }
 
   // ---- epilogue: lane (li, g) holds d = 32 mb + 16 g + r of head li ----
-  if (!hvalid) return;
+  if (!hvalid) return false;
   if (splits == 1) {
-    const float inv = 1.f / l_w;
+    const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
     uint16_t* orow = out + ((size_t)t * H + h) * DV + 16 * g;
 #pragma unroll
     for (int mb = 0; mb < 16; ++mb) {
@@ -418,47 +437,30 @@ __device__ __forceinline__ void attend_unit(
     if (g == 0)
       reinterpret_cast<float4*>(ws_ml)[(size_t)slot * H + h] = make_float4(m_run, l_w, l_e, 0.f);
   }
+  return false;
 }
 
 }  // namespace sas
 
 namespace sas {
 
-// First pass: one workgroup per work unit.
+// One workgroup per work unit.
 template <int DQK, int QT>
 __global__ __launch_bounds__(256, 1) void attend_kernel(
     SasFwdArgs a, const uint16_t* __restrict__ q, const uint8_t* __restrict__ ori_kv,
     const uint8_t* __restrict__ cmp_kv, const int* __restrict__ cmp_bt,
     const int* __restrict__ rows_list, const int* __restrict__ ncmp,
     const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
-    float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    int* __restrict__ redo_flags, float* __restrict__ redo_m) {
+    float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   __shared__ __attribute__((aligned(16))) AttendLds<DQK> sm;
   const int u = blockIdx.x;
   if (plan[PH_MAGIC] != SAS_PLAN_MAGIC || u >= plan[PH_UNITS]) return;
-  attend_unit<DQK, QT, false>(u, sm, a, q, ori_kv, cmp_kv, cmp_bt, rows_list, ncmp, sinks, plan,
-                              out, lse, ws_o, ws_ml, redo_flags, redo_m);
-}
-
-// Redo pass: a grid of about one workgroup per CU strides over the units and
-// recomputes the flagged ones (normally none: every workgroup exits after
-// scanning its share of the flags).
-template <int DQK, int QT>
-__global__ __launch_bounds__(256, 1) void attend_redo_kernel(
-    SasFwdArgs a, const uint16_t* __restrict__ q, const uint8_t* __restrict__ ori_kv,
-    const uint8_t* __restrict__ cmp_kv, const int* __restrict__ cmp_bt,
-    const int* __restrict__ rows_list, const int* __restrict__ ncmp,
-    const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
-    float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    int* __restrict__ redo_flags, float* __restrict__ redo_m) {
-  __shared__ __attribute__((aligned(16))) AttendLds<DQK> sm;
-  if (plan[PH_MAGIC] != SAS_PLAN_MAGIC) return;
-  const int units = plan[PH_UNITS];
-  for (int u = blockIdx.x; u < units; u += gridDim.x) {
-    if (redo_flags[u] == 0) continue;
-    __syncthreads();  // the previous unit is done with the shared tiles
-    attend_unit<DQK, QT, true>(u, sm, a, q, ori_kv, cmp_kv, cmp_bt, rows_list, ncmp, sinks,
-                               plan, out, lse, ws_o, ws_ml, redo_flags, redo_m);
+  float m_obs = 0.f;
+  if (attend_unit<DQK, QT, false>(u, sm, a, q, ori_kv, cmp_kv, cmp_bt, rows_list, ncmp, sinks,
+                                  plan, out, lse, ws_o, ws_ml, m_obs)) {
+    lds_barrier();  // every wave is done with the ring before the redo refills it
+    attend_unit<DQK, QT, true>(u, sm, a, q, ori_kv, cmp_kv, cmp_bt, rows_list, ncmp, sinks, plan,
+                               out, lse, ws_o, ws_ml, m_obs);
   }
 }
 

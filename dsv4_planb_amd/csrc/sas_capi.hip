@@ -19,6 +19,10 @@ namespace {
 
 int esize(int dt) { return dt == SAS_DT_FP8E4M3 ? 1 : 2; }
 
+// Compressed slots per token: top-k index slots (scenario 3) or the compressed
+// row-list capacity (scenario 2).
+int list_k(const sas_params_t* p) { return p->scenario >= 2 ? p->topk : 0; }
+
 int query_num_cus() {
   int dev = 0, n = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
@@ -42,7 +46,7 @@ SasFwdArgs fwd_args(const sas_params_t* p, int target) {
   a.H = p->num_heads_q;
   a.B = p->batch;
   a.scenario = p->scenario;
-  a.K = p->scenario == 3 ? p->topk : 0;
+  a.K = list_k(p);
   a.cmp_ratio = p->cmp_ratio > 0 ? p->cmp_ratio : 1;
   a.ori_block_size = p->ori_block_size;
   a.ori_table_len = p->ori_table_len;
@@ -69,7 +73,7 @@ SasPlanArgs plan_args(const sas_params_t* p, int target) {
   a.scenario = p->scenario;
   a.win_left = p->ori_win_left;
   a.cmp_ratio = p->cmp_ratio > 0 ? p->cmp_ratio : 1;
-  a.K = p->scenario == 3 ? p->topk : 0;
+  a.K = list_k(p);
   a.H = p->num_heads_q;
   a.target = target;
   return a;
@@ -97,12 +101,10 @@ struct Ws {
   int* plan;
   float* o;
   float* ml;
-  int* flags;
-  float* redo_m;
 };
 
 int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out) {
-  const SasWsLayout W = sas_ws_layout(p->total_tokens, p->scenario == 3 ? p->topk : 0,
+  const SasWsLayout W = sas_ws_layout(p->total_tokens, list_k(p),
                                       p->num_heads_q, p->head_dim_v, target, p->scenario,
                                       p->ori_win_left);
   if (!ws || ws_bytes < W.total) return SAS_ERR_WORKSPACE;
@@ -113,8 +115,6 @@ int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out)
   out->plan = reinterpret_cast<int*>(base + W.off_plan);
   out->o = reinterpret_cast<float*>(base + W.off_o);
   out->ml = reinterpret_cast<float*>(base + W.off_ml);
-  out->flags = reinterpret_cast<int*>(base + W.off_flags);
-  out->redo_m = reinterpret_cast<float*>(base + W.off_redo_m);
   return SAS_OK;
 }
 
@@ -149,15 +149,10 @@ fwd_fn_t pick_fwd(const sas_params_t* p) {
 
 typedef void (*attend_fn_t)(SasFwdArgs, const uint16_t*, const uint8_t*, const uint8_t*,
                             const int*, const int*, const int*, const float*, const int*,
-                            uint16_t*, float*, float*, float*, int*, float*);
+                            uint16_t*, float*, float*, float*);
 
-attend_fn_t pick_attend(const sas_params_t* p, bool redo) {
+attend_fn_t pick_attend(const sas_params_t* p) {
   const bool f16 = p->q_dtype == SAS_DT_FP16;
-  if (redo) {
-    if (p->head_dim_qk == 576)
-      return f16 ? &sas::attend_redo_kernel<576, 1> : &sas::attend_redo_kernel<576, 0>;
-    return f16 ? &sas::attend_redo_kernel<512, 1> : &sas::attend_redo_kernel<512, 0>;
-  }
   if (p->head_dim_qk == 576)
     return f16 ? &sas::attend_kernel<576, 1> : &sas::attend_kernel<576, 0>;
   return f16 ? &sas::attend_kernel<512, 1> : &sas::attend_kernel<512, 0>;
@@ -219,8 +214,9 @@ int sas_validate(const sas_params_t* p) {
       return SAS_ERR_SHAPE;
     if ((int64_t)p->cmp_block_num * p->cmp_block_size >= (int64_t)1 << 31) return SAS_ERR_SHAPE;
   }
-  if (p->scenario == 3 && p->topk < 1) return SAS_ERR_SCENARIO;
-  if ((int64_t)p->total_tokens * (p->scenario == 3 ? p->topk : 1) >= (int64_t)1 << 31)
+  if (p->scenario >= 2 && p->topk < 1) return SAS_ERR_SCENARIO;
+  if ((int64_t)p->total_tokens * sas_row_list_stride(p->ori_win_left, list_k(p), p->scenario) >=
+      (int64_t)1 << 31)
     return SAS_ERR_SHAPE;
   return SAS_OK;
 }
@@ -243,7 +239,7 @@ int sas_workspace_size(const sas_params_t* p, size_t* bytes) {
   int rc = sas_validate(p);
   if (rc) return rc;
   if (!bytes) return SAS_ERR_NULL;
-  *bytes = sas_ws_layout(p->total_tokens, p->scenario == 3 ? p->topk : 0, p->num_heads_q,
+  *bytes = sas_ws_layout(p->total_tokens, list_k(p), p->num_heads_q,
                          p->head_dim_v, target_units(p), p->scenario, p->ori_win_left)
                .total;
   return SAS_OK;
@@ -271,9 +267,9 @@ int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   if ((rc = carve(p, ws, ws_bytes, target, &w))) return rc;
   if (!plan) plan = w.plan;
   if (p->total_tokens == 0) return SAS_OK;
-  hipLaunchKernelGGL(sas::resolve_kernel, dim3(p->total_tokens), dim3(64), 0, (hipStream_t)stream,
-                     fwd_args(p, target), plan, t->ori_block_table, t->cmp_sparse_indices,
-                     t->cmp_block_table, w.rows, w.ncmp, w.flags);
+  hipLaunchKernelGGL(sas::resolve_kernel, dim3(p->total_tokens), dim3(sas::RS_NT), 0,
+                     (hipStream_t)stream, fwd_args(p, target), plan, t->ori_block_table,
+                     t->cmp_sparse_indices, t->cmp_block_table, w.rows, w.ncmp);
   return launch_status();
 }
 
@@ -289,20 +285,11 @@ int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pla
   if (p->total_tokens == 0) return SAS_OK;
   const SasFwdArgs a = fwd_args(p, target);
   if (p->kv_dtype != SAS_DT_FP8E4M3) {
-    // first pass, then the redo pass for units whose logits outgrew their frame
-    const int redo_grid = std::min(a.unit_cap, std::max(1, query_num_cus()));
-    for (int redo = 0; redo < 2; ++redo) {
-      attend_fn_t fn = pick_attend(p, redo != 0);
-      hipLaunchKernelGGL(fn, dim3(redo ? redo_grid : a.unit_cap), dim3(256), 0,
-                         (hipStream_t)stream, a,
-                         static_cast<const uint16_t*>(t->q),
-                         static_cast<const uint8_t*>(t->ori_kv),
-                         static_cast<const uint8_t*>(t->cmp_kv), t->cmp_block_table, w.rows,
-                         w.ncmp, t->sinks, plan, static_cast<uint16_t*>(t->out), t->lse, w.o,
-                         w.ml, w.flags, w.redo_m);
-      if ((rc = launch_status())) return rc;
-    }
-    return SAS_OK;
+    hipLaunchKernelGGL(pick_attend(p), dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream, a,
+                       static_cast<const uint16_t*>(t->q), static_cast<const uint8_t*>(t->ori_kv),
+                       static_cast<const uint8_t*>(t->cmp_kv), t->cmp_block_table, w.rows,
+                       w.ncmp, t->sinks, plan, static_cast<uint16_t*>(t->out), t->lse, w.o, w.ml);
+    return launch_status();
   }
   fwd_fn_t fn = pick_fwd(p);
   hipLaunchKernelGGL(fn, dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream, a,
@@ -324,7 +311,8 @@ int sas_combine(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   if (!plan) plan = w.plan;
   if (p->total_tokens == 0) return SAS_OK;
   const SasFwdArgs a = fwd_args(p, target);
-  const dim3 grid(target, (p->num_heads_q + sas::COMBINE_HEADS - 1) / sas::COMBINE_HEADS);
+  const int groups = (p->num_heads_q + sas::COMBINE_HEADS - 1) / sas::COMBINE_HEADS;
+  const dim3 grid(std::min(target * groups, 2 * std::max(1, query_num_cus())));
   const dim3 block(64 * sas::COMBINE_HEADS);
   if (p->q_dtype == SAS_DT_BF16)
     hipLaunchKernelGGL(sas::combine_kernel<0>, grid, block, 0, (hipStream_t)stream, a, plan, w.o,
@@ -360,7 +348,7 @@ int sas_debug_rows(const sas_params_t* p, const void* ws, int32_t* rows, int32_t
   int rc = sas_validate(p);
   if (rc) return rc;
   if (!ws || !rows || !counts) return SAS_ERR_NULL;
-  const int K = p->scenario == 3 ? p->topk : 0;
+  const int K = list_k(p);
   const SasWsLayout W = sas_ws_layout(p->total_tokens, K, p->num_heads_q, p->head_dim_v,
                                       target_units(p), p->scenario, p->ori_win_left);
   const size_t stride = (size_t)sas_row_list_stride(p->ori_win_left, K, p->scenario);

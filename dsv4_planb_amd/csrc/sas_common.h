@@ -54,16 +54,17 @@ SAS_HD static inline SasPlanLayout sas_plan_layout(int64_t T, int64_t target) {
 
 // ---- workspace (bytes, each region 256-B aligned) ----
 struct SasWsLayout {
-  size_t off_rows, off_ncmp, off_plan, off_o, off_ml, off_flags, off_redo_m, total;
+  size_t off_rows, off_ncmp, off_plan, off_o, off_ml, total;
   int64_t slot_cap;
 };
 
 SAS_HD static inline size_t sas_align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Row-code list of one token: window rows (win_left + 1 slots) then, in scenario 3,
-// the resolved compressed rows (topk slots).
+// Row-code list of one token: its window rows, then directly after them its
+// compressed rows (scenario 3: the resolved top-k; scenario 2: every causally
+// valid row, up to K of them).  Capacity: win_left + 1 + K slots.
 SAS_HD static inline int64_t sas_row_list_stride(int64_t win_left, int64_t K, int scenario) {
-  return win_left + 1 + (scenario == 3 ? K : 0);
+  return win_left + 1 + (scenario >= 2 ? K : 0);
 }
 
 SAS_HD static inline SasWsLayout sas_ws_layout(int64_t T, int64_t K, int64_t H, int64_t Dv,
@@ -83,12 +84,6 @@ SAS_HD static inline SasWsLayout sas_ws_layout(int64_t T, int64_t K, int64_t H, 
   off = sas_align256(off + (size_t)W.slot_cap * H * Dv * 4);
   W.off_ml = off;  // per (slot, head): float4 (m, l_w, l_e, 0)
   off = sas_align256(off + (size_t)W.slot_cap * H * 4 * 4);
-  // overflow guard of the attention kernel: per-unit flag, per (unit, head) maximum
-  const int64_t units = sas_plan_layout(T, target).unit_cap;
-  W.off_flags = off;
-  off = sas_align256(off + (size_t)units * 4);
-  W.off_redo_m = off;
-  off = sas_align256(off + (size_t)units * H * 4);
   W.total = off;
   return W;
 }
@@ -101,7 +96,7 @@ struct SasPlanArgs {
 struct SasFwdArgs {
   int32_t T, H, B;
   int32_t scenario, K, cmp_ratio;
-  int32_t win_left, list_stride;  // row-code list: win_left + 1 window slots (+ K)
+  int32_t win_left, list_stride;  // row-code list capacity: win_left + 1 (+ K)
   int32_t ori_block_size, ori_table_len, ori_block_num;
   int32_t cmp_block_size, cmp_table_len, cmp_block_num;
   int64_t ori_block_stride, ori_row_stride, cmp_block_stride, cmp_row_stride;  // elements

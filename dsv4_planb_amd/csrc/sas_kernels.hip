@@ -71,7 +71,7 @@ __device__ TokInfo token_info(const SasPlanArgs& a, const int* __restrict__ q_pr
   int ncmp = 0;
   if (a.scenario >= 2) {
     int thr = floor_div(sg + 1, a.cmp_ratio);         // golden.py:44, 147
-    ncmp = a.scenario == 3 ? min(a.K, thr) : thr;     // golden.py:48 / 148
+    ncmp = a.K > 0 ? min(a.K, thr) : thr;             // golden.py:48 / 148 (list capacity)
     ncmp = max(ncmp, 0);
   }
   ti.b = b;
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
 }
 
 // ===========================================================================
-// Row resolution, one wave per token.  Writes the token's row-code list: the
+// Row resolution.  Writes each token's row-code list: the
 // window rows (golden.py:129-131, paged as golden.py:247-268) and, in scenario 3,
 // the resolved compressed rows (golden.py:28-66).  A code is a flat pool row
 // (page * block_size + offset) or -1 for a row the reference reads as zeros
@@ -209,56 +209,89 @@ __device__ __forceinline__ int paged_code(const int* __restrict__ bt_row, int ta
   return (page < 0 || page >= block_num) ? -1 : page * block_size + (pos - blk * block_size);
 }
 
-__global__ __launch_bounds__(64) void resolve_kernel(SasFwdArgs a, const int* __restrict__ plan,
-                                                     const int* __restrict__ ori_bt,
-                                                     const int* __restrict__ idx,
-                                                     const int* __restrict__ cmp_bt,
-                                                     int* __restrict__ rows_out,
-                                                     int* __restrict__ ncmp_out,
-                                                     int* __restrict__ redo_flags) {
+// One workgroup (256 threads) per token.  Thread i owns index slots
+// [RS_PER i, RS_PER (i + 1)) of the first min(K, thr) slots; the first -1 (a
+// block-wide minimum) ends the list, ids outside [0, thr) are skipped, and the
+// survivors keep their slot order through a block-wide exclusive scan.
+constexpr int RS_NT = 256;
+
+__global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int* __restrict__ plan,
+                                                        const int* __restrict__ ori_bt,
+                                                        const int* __restrict__ idx,
+                                                        const int* __restrict__ cmp_bt,
+                                                        int* __restrict__ rows_out,
+                                                        int* __restrict__ ncmp_out) {
+  __shared__ int s_term;
+  __shared__ int s_wsum[RS_NT / 64];
   const int t = blockIdx.x;
-  const int lane = threadIdx.x;
-  // clear the attention kernel's per-unit overflow flags (unit_cap of them over T blocks)
-  const int per = (a.unit_cap + a.T - 1) / a.T;
-  for (int i = lane; i < per; i += 64)
-    if (t * per + i < a.unit_cap) redo_flags[t * per + i] = 0;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
   const int b = tk[TK_B];
   if (b < 0) {
-    if (lane == 0) ncmp_out[t] = 0;
+    if (tid == 0) ncmp_out[t] = 0;
     return;
   }
   int* out = rows_out + (size_t)t * a.list_stride;
   const int nwin = tk[TK_NWIN], winlo = tk[TK_WINLO];
   const int* obt = ori_bt + (size_t)b * a.ori_table_len;
-  for (int r = lane; r < nwin; r += 64)
+  for (int r = tid; r < nwin; r += RS_NT)
     out[r] = paged_code(obt, a.ori_table_len, a.ori_block_size, a.ori_block_num, winlo + r);
-  if (a.scenario != 3) {
-    if (lane == 0) ncmp_out[t] = a.scenario == 2 ? tk[TK_NCMPMAX] : 0;
+  if (a.scenario == 1) {
+    if (tid == 0) ncmp_out[t] = 0;
     return;
   }
-  out += a.win_left + 1;
+  out += nwin;  // compressed codes follow the window codes
   const int thr = floor_div(tk[TK_SG] + 1, a.cmp_ratio);
+  if (a.scenario == 2) {  // golden.py:146-150: every compressed row below thr
+    const int n = max(min(thr, a.K), 0);
+    const int* cbt2 = cmp_bt + (size_t)b * a.cmp_table_len;
+    for (int j = tid; j < n; j += RS_NT)
+      out[j] = paged_code(cbt2, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, j);
+    if (tid == 0) ncmp_out[t] = n;
+    return;
+  }
   const int limit = max(min(a.K, thr), 0);  // golden.py:48
   const int* ir = idx + (size_t)t * a.K;
-  const int* cbt = cmp_bt + (size_t)b * a.cmp_table_len;
-  int count = 0;
-  for (int base = 0; base < limit; base += 64) {
-    const int i = base + lane;
-    const bool in = i < limit;
-    const int id = in ? ir[i] : 0;
-    const unsigned long long term = __ballot(in && id == -1);  // golden.py:52-53
-    bool valid = in && id >= 0 && id < thr;                     // golden.py:58-59
-    if (term) valid = valid && lane < (__ffsll((long long)term) - 1);
-    const unsigned long long vm = __ballot(valid);
-    if (valid) {
-      const int pos = count + __popcll(vm & ((1ull << lane) - 1ull));
-      out[pos] = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, id);
+  const int per = (limit + RS_NT - 1) / RS_NT;
+  const int s0 = min(tid * per, limit), s1 = min(s0 + per, limit);
+  if (tid == 0) s_term = limit;
+  __syncthreads();
+  // golden.py:52-53: the first -1 terminates the list
+  for (int i = s0; i < s1; ++i)
+    if (ir[i] == -1) {
+      atomicMin(&s_term, i);
+      break;
     }
-    count += __popcll(vm);
-    if (term) break;
+  __syncthreads();
+  const int term = s_term;
+  int cnt = 0;
+  for (int i = s0; i < min(s1, term); ++i) {
+    const int id = ir[i];
+    cnt += (id >= 0 && id < thr);  // golden.py:58-59: ids at or beyond thr are skipped
   }
-  if (lane == 0) ncmp_out[t] = count;
+  // block-wide exclusive scan of cnt
+  int incl = cnt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off);
+    if (lane >= off) incl += v;
+  }
+  if (lane == 63) s_wsum[w] = incl;
+  __syncthreads();
+  int base = incl - cnt;
+  for (int j = 0; j < w; ++j) base += s_wsum[j];
+  const int* cbt = cmp_bt + (size_t)b * a.cmp_table_len;
+  for (int i = s0; i < min(s1, term); ++i) {
+    const int id = ir[i];
+    if (id >= 0 && id < thr)
+      out[base++] = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, id);
+  }
+  if (tid == RS_NT - 1) {
+    int total = 0;
+    for (int j = 0; j < RS_NT / 64; ++j) total += s_wsum[j];
+    ncmp_out[t] = total;
+  }
 }
 
 // ===========================================================================
@@ -283,6 +316,19 @@ __device__ __forceinline__ uint32_t to_q16(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
+// Two floats -> two 16-bit values of the query dtype (round to nearest even),
+// packed low = a, high = b: one v_cvt_pk_bf16_f32 for bf16.
+template <int QT>
+__device__ __forceinline__ uint32_t pack2_q16(float a, float b) {
+  if constexpr (QT == 0) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, b2{(__bf16)a, (__bf16)b});
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, h2{(_Float16)a, (_Float16)b});
+  }
+}
+
 // 16-bit payload of the query dtype -> float (exact).
 template <int QT>
 __device__ __forceinline__ float q16_to_f32(uint32_t v) {
@@ -290,6 +336,20 @@ __device__ __forceinline__ float q16_to_f32(uint32_t v) {
     return __uint_as_float(v << 16);
   else
     return (float)__builtin_bit_cast(_Float16, (uint16_t)v);
+}
+
+// acc + the two 16-bit values packed in v (exact products with 1, fp32 sum).
+template <int QT>
+__device__ __forceinline__ float sum2_q16(uint32_t v, float acc) {
+  if constexpr (QT == 0) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 one = {(__bf16)1.f, (__bf16)1.f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, v), one, acc, false);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 one = {(_Float16)1.f, (_Float16)1.f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v), one, acc, false);
+  }
 }
 
 // OCP FP8 E4M3FN code -> exact 16-bit value of the query dtype.
@@ -375,14 +435,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
   const int* codes = rows_list + (size_t)t * a.list_stride;
 
   // Row code of list row r (-1 = zero row); window rows first, then compressed rows.
-  auto row_code = [&](int r) -> int {
-    if (r >= r1) return -1;
-    if (r < nwin) return codes[r];
-    const int j = r - nwin;
-    if (a.scenario == 3) return codes[a.win_left + 1 + j];
-    return paged_code(cmp_bt + (size_t)b * a.cmp_table_len, a.cmp_table_len, a.cmp_block_size,
-                      a.cmp_block_num, j);  // scenario 2: every compressed row below thr
-  };
+  auto row_code = [&](int r) -> int { return r < r1 ? codes[r] : -1; };
   auto row_ptr = [&](int r, int code) -> const uint8_t* {
     if (code < 0) return g_zero_row;
     if (r < nwin) {
@@ -643,7 +696,8 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
 }
 
 // ===========================================================================
-// Split combine: one wave per (split token, head); lane l merges columns
+// Split combine: one wave per (split token, head), grid-stride over the split
+// tokens the plan recorded (none: every workgroup exits); lane l merges columns
 // [8 l, 8 l + 8) of the d_v = 512 partial outputs.  A partial holds O and its
 // two normalisers (l_w: sum of the rounded P that entered O, for the output;
 // l_e: sum of the exact P, for the LSE) in its own frame m; the merge rescales
@@ -656,40 +710,43 @@ __global__ __launch_bounds__(64 * COMBINE_HEADS) void combine_kernel(
     SasFwdArgs a, const int* __restrict__ plan, const float* __restrict__ ws_o,
     const float* __restrict__ ws_ml, uint16_t* __restrict__ out, float* __restrict__ lse) {
   constexpr int DV = 512;
-  const int i = blockIdx.x;
-  if (i >= plan[PH_NSPLIT_TOKENS]) return;
   const int H = a.H;
-  const int h = blockIdx.y * COMBINE_HEADS + (threadIdx.x >> 6);
-  if (h >= H) return;
+  const int groups = (H + COMBINE_HEADS - 1) / COMBINE_HEADS;
+  const int items = plan[PH_NSPLIT_TOKENS] * groups;  // (split token, head group) pairs
   const int lane = threadIdx.x & 63;
   const SasPlanLayout L = sas_plan_layout(a.T, a.split_cap);
-  const int t = plan[L.off_split_tokens + i];
-  const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
-  const int S = tk[TK_SPLITS], base = tk[TK_WSBASE];
   const float4* ml = reinterpret_cast<const float4*>(ws_ml);
-  float mx = -INFINITY;
-  for (int s = 0; s < S; ++s) mx = fmaxf(mx, ml[(size_t)(base + s) * H + h].x);
-  float l = 0.f, le = 0.f;
-  float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
-  for (int s = 0; s < S; ++s) {
-    const size_t row = (size_t)(base + s) * H + h;
-    const float4 rec = ml[row];
-    const float wgt = rec.x == -INFINITY ? 0.f : exp2f(rec.x - mx);
-    l += wgt * rec.y;
-    le += wgt * rec.z;
-    const float4* src = reinterpret_cast<const float4*>(ws_o + row * DV) + 2 * lane;
-    const float4 v0 = src[0], v1 = src[1];
-    o0.x += wgt * v0.x; o0.y += wgt * v0.y; o0.z += wgt * v0.z; o0.w += wgt * v0.w;
-    o1.x += wgt * v1.x; o1.y += wgt * v1.y; o1.z += wgt * v1.z; o1.w += wgt * v1.w;
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    const int i = item / groups;
+    const int h = (item - i * groups) * COMBINE_HEADS + (threadIdx.x >> 6);
+    if (h >= H) continue;
+    const int t = plan[L.off_split_tokens + i];
+    const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
+    const int S = tk[TK_SPLITS], base = tk[TK_WSBASE];
+    float mx = -INFINITY;
+    for (int s = 0; s < S; ++s) mx = fmaxf(mx, ml[(size_t)(base + s) * H + h].x);
+    float l = 0.f, le = 0.f;
+    float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
+    for (int s = 0; s < S; ++s) {
+      const size_t row = (size_t)(base + s) * H + h;
+      const float4 rec = ml[row];
+      const float wgt = rec.x == -INFINITY ? 0.f : exp2f(rec.x - mx);
+      l += wgt * rec.y;
+      le += wgt * rec.z;
+      const float4* src = reinterpret_cast<const float4*>(ws_o + row * DV) + 2 * lane;
+      const float4 v0 = src[0], v1 = src[1];
+      o0.x += wgt * v0.x; o0.y += wgt * v0.y; o0.z += wgt * v0.z; o0.w += wgt * v0.w;
+      o1.x += wgt * v1.x; o1.y += wgt * v1.y; o1.z += wgt * v1.z; o1.w += wgt * v1.w;
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    u32x4_t o;
+    o[0] = to_q16<QT>(o0.x * inv) | (to_q16<QT>(o0.y * inv) << 16);
+    o[1] = to_q16<QT>(o0.z * inv) | (to_q16<QT>(o0.w * inv) << 16);
+    o[2] = to_q16<QT>(o1.x * inv) | (to_q16<QT>(o1.y * inv) << 16);
+    o[3] = to_q16<QT>(o1.z * inv) | (to_q16<QT>(o1.w * inv) << 16);
+    reinterpret_cast<u32x4_t*>(out + ((size_t)t * H + h) * DV)[lane] = o;
+    if (lse && lane == 0) lse[(size_t)t * H + h] = (mx + __log2f(le)) * 0.6931471805599453f;
   }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  u32x4_t o;
-  o[0] = to_q16<QT>(o0.x * inv) | (to_q16<QT>(o0.y * inv) << 16);
-  o[1] = to_q16<QT>(o0.z * inv) | (to_q16<QT>(o0.w * inv) << 16);
-  o[2] = to_q16<QT>(o1.x * inv) | (to_q16<QT>(o1.y * inv) << 16);
-  o[3] = to_q16<QT>(o1.z * inv) | (to_q16<QT>(o1.w * inv) << 16);
-  reinterpret_cast<u32x4_t*>(out + ((size_t)t * H + h) * DV)[lane] = o;
-  if (lse && lane == 0) lse[(size_t)t * H + h] = (mx + __log2f(le)) * 0.6931471805599453f;
 }
 
 }  // namespace sas

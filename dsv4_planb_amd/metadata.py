@@ -117,7 +117,7 @@ def plan_params(*, total_tokens, batch, num_heads_q, scenario, topk, cmp_ratio, 
     p.cmp_block_num = p.cmp_block_size = p.cmp_table_len = 1
     p.ori_block_stride = p.ori_row_stride = p.head_dim_qk
     p.cmp_block_stride = p.cmp_row_stride = p.head_dim_qk
-    p.topk = topk if scenario == 3 else 0
+    p.topk = topk if scenario >= 2 else 0  # scenario 2: bound on compressed rows per token
     p.cmp_ratio = max(cmp_ratio, 1)
     p.scenario = scenario
     p.ori_win_left, p.ori_win_right = ori_win_left, 0
@@ -220,7 +220,11 @@ def sparse_attn_sharedkv_metadata(
         if seqused_q is not None and seqused_q.numel() > 0:
             act_q = seqused_q.to(dev, torch.int32)
     scenario = 1 if not has_cmp_kv else (3 if cmp_topk > 0 else 2)
+    topk = cmp_topk
+    if scenario == 2:  # bound on the causally valid compressed rows of any token
+        kv_max = max_seqlen_kv if max_seqlen_kv > 0 else int(seqused_kv.max().item())
+        topk = max(kv_max // max(cmp_ratio, 1), 1)
     p = plan_params(total_tokens=total, batch=batch, num_heads_q=num_heads_q, scenario=scenario,
-                    topk=cmp_topk, cmp_ratio=cmp_ratio, ori_win_left=ori_win_left,
+                    topk=topk, cmp_ratio=cmp_ratio, ori_win_left=ori_win_left,
                     core_num=aic_core_num, head_dim=head_dim)
     return device_plan(p, q_prefix, act_q, seqused_kv.to(dev))

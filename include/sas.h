@@ -73,7 +73,10 @@ typedef struct {
   int64_t ori_block_stride;  /* elements between pages of ori_kv (>= block_size*row_stride) */
   int64_t ori_row_stride;    /* elements between rows of a page (>= head_dim_qk) */
   int64_t cmp_block_stride, cmp_row_stride;
-  int32_t topk;              /* K: index slots per token (scenario 3) */
+  int32_t topk;              /* scenario 3: K index slots per token; scenario 2: capacity of the
+                                per-token list of causally valid compressed rows (rows past it
+                                are not attended; cmp_table_len * cmp_block_size covers every
+                                row the block table maps) */
   int32_t cmp_ratio;         /* compression ratio (scenarios 2, 3) */
   int32_t scenario;          /* 1 SWA, 2 CFA, 3 SCFA */
   int32_t ori_win_left;      /* 0..127 (reference: 127) */
@@ -133,8 +136,9 @@ int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pla
 int sas_combine(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
                 void* workspace, size_t workspace_bytes, sas_stream_t stream);
 /* Debug: copy the resolved row-code lists of every token into rows (int32
- * [T, win_left + 1 (+ topk in scenario 3)]: window pool rows, then compressed pool
- * rows; -1 = a row read as zeros) and the compressed-row counts into counts [T]. */
+ * [T, win_left + 1 (+ topk in scenarios 2, 3)]: the token's window pool rows, then
+ * directly after them its compressed pool rows; -1 = a row read as zeros) and the
+ * compressed-row counts into counts [T]. */
 int sas_debug_rows(const sas_params_t* p, const void* workspace, int32_t* rows, int32_t* counts,
                    sas_stream_t stream);
 
