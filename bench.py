@@ -198,7 +198,7 @@ def measure(wl, steps, warmup, core_num=256):
 def _traffic_from_profile(workload):
     """HBM bytes per attention launch measured with rocprofv3 counters, if a
     summary for this workload is committed (profiles/<kernel>_<workload>_pmc.json)."""
-    path = os.path.join(ROOT, "profiles", f"sas_fwd_{workload}_pmc.json")
+    path = os.path.join(ROOT, "profiles", f"sas_attend_{workload}_pmc.json")
     if not os.path.exists(path):
         return None
     try:
@@ -313,8 +313,8 @@ def main_r_batch(name):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="decode128k",
                     choices=["decode128k", "prefill8k", "decode32"])
     ap.add_argument("--extra", default="prefill8k,decode32",
@@ -374,7 +374,7 @@ def main():
         ach, peak, unit = main_r["attend_tflops"], MFMA_BF16_PEAK_TFLOPS, "TFLOP/s"
     roofline = {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
                 "frac": round(ach / peak, 4), "traffic": _traffic_from_profile(args.workload),
-                "kernel": "sas::fwd_kernel", "kernel_us": round(main_r["attend_us"], 2),
+                "kernel": "sas::attend_kernel<576, bf16>", "kernel_us": round(main_r["attend_us"], 2),
                 "algorithmic_bytes": main_r["alg_bytes"], "algorithmic_flops": main_r["alg_flops"]}
     cpu = None
     if not args.no_cpu_baseline:
