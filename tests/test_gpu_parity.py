@@ -175,3 +175,136 @@ def test_resolution_bit_exact():
         np.testing.assert_array_equal(rows[t, :no], ref[t, :no])
         # compressed codes follow the window codes directly
         np.testing.assert_array_equal(rows[t, no:no + nc], ref[t, no:no + nc])
+
+
+# ---- layouts on the wire (reference api.py:223-240, perf_compare.py:220-247) ----
+def test_bsnd_layout_with_ragged_cu_seqlens():
+    """BSND q ``[B, S, H, D]`` with cu_seqlens_q giving per-batch lengths below S
+    (api.py:223-240): token (b, s) lives at flat row b*S + s; rows past a batch's
+    length are padding and come back as zeros."""
+    import dataclasses
+
+    from dsv4_planb_amd import sparse_attn_sharedkv
+
+    B, S, H, K = 3, 4, 64, 256
+    c = make_case(B=B, H=H, seq_kv=[3000, 700, 9000], q_per_seq=[4, 2, 3], scenario=3, K=K,
+                  seed=13)
+    T = B * S
+    q_pad = np.zeros((T, H, c.D), c.q_bits.dtype)
+    idx_pad = np.full((T, K), -1, np.int32)
+    for b in range(B):
+        lo, n = int(c.cu_seqlens_q[b]), int(c.act_q[b])
+        q_pad[b * S:b * S + n] = c.q_bits[lo:lo + n]
+        idx_pad[b * S:b * S + n] = c.idx[lo:lo + n]
+    cb = dataclasses.replace(c, T=T, q_bits=q_pad, idx=idx_pad,
+                             q_prefix=np.arange(B, dtype=np.int32) * S)
+    _banner("bsnd", cb)
+    d = to_device(c)
+    q = torch.from_numpy(q_pad.view(np.int16)).view(torch.bfloat16).reshape(B, S, H, c.D).cuda()
+    idx = torch.from_numpy(idx_pad).reshape(B, S, 1, K).cuda()
+    out, lse = sparse_attn_sharedkv(
+        q, ori_kv=d["ori_kv"], cmp_kv=d["cmp_kv"], cmp_sparse_indices=idx,
+        ori_block_table=d["ori_block_table"], cmp_block_table=d["cmp_block_table"],
+        cu_seqlens_q=d["cu_seqlens_q"], seqused_kv=d["seqused_kv"], sinks=d["sinks"],
+        softmax_scale=c.softmax_scale, cmp_ratio=4, layout_q="BSND", return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (B, S, H, 512) and tuple(lse.shape) == (B, S, H)
+    out = out.float().cpu().numpy().reshape(T, H, 512)
+    lse = lse.cpu().numpy().reshape(T, H)
+    ref, ref_lse = cb.oracle_c()
+    ex, ex_lse = cb.oracle_exact()
+    for b in range(B):  # padding rows: zero output and zero lse, like the oracle's
+        n = int(c.act_q[b])
+        assert not out[b * S + n:(b + 1) * S].any() and not lse[b * S + n:(b + 1) * S].any()
+    assert_parity(out, lse, ref, ref_lse, label="bsnd", exact=(ex, ex_lse))
+
+
+def test_padded_page_strides():
+    """Paged pools with padded block and row strides, as the Ascend stride-padded
+    layout has (perf_compare.py:220-247): the kernel addresses rows through the
+    strides, without a repacking copy."""
+    c = make_case(B=2, H=32, seq_kv=[5000, 1300], q_per_seq=2, scenario=3, K=512, seed=14)
+    _banner("strides", c)
+    d = to_device(c)
+
+    def padded(pool):
+        nb, bs, _, D = pool.shape
+        base = torch.full((nb, bs + 3, 1, D + 64), float("nan"), dtype=pool.dtype, device=pool.device)
+        view = base[:, :bs, :, :D]
+        view.copy_(pool)
+        return view
+
+    d["ori_kv"] = padded(d["ori_kv"])
+    d["cmp_kv"] = padded(d["cmp_kv"])
+    assert not d["ori_kv"].is_contiguous() and d["ori_kv"].stride(1) == c.D + 64
+    from dsv4_planb_amd import sparse_attn_sharedkv
+
+    q = d.pop("q")
+    out, lse = sparse_attn_sharedkv(q, softmax_scale=c.softmax_scale, cmp_ratio=4,
+                                    return_softmax_lse=True, topk_cmp=c.K, **d)
+    torch.cuda.synchronize()
+    ref, ref_lse = c.oracle_c()
+    ex, ex_lse = c.oracle_exact()
+    assert_parity(out.float().cpu().numpy(), lse.cpu().numpy(), ref, ref_lse, label="strides",
+                  exact=(ex, ex_lse))
+
+
+# ---- the device split-KV plan (no counterpart in the reference: property checks) ----
+@pytest.mark.parametrize("cores", [256, 1024, 4096])
+def test_device_plan_covers_every_row_once(cores):
+    """Every token's row list [0, window + compressed capacity) is covered by its
+    units exactly once, in split order; split tokens own disjoint workspace slots;
+    padding tokens get one empty unit."""
+    from dsv4_planb_amd import metadata as M
+
+    rng = np.random.default_rng(cores)
+    B, S = 9, 40
+    act_q = rng.integers(0, S + 1, size=B)
+    act_q[0] = S
+    kv = rng.integers(1, 70000, size=B)
+    kv = np.maximum(kv, act_q)
+    K = 2048
+    cu = np.zeros(B + 1, np.int32)
+    cu[1:] = np.cumsum(act_q)
+    T = int(cu[-1])
+    print(f"\n[case] plan: cores={cores} B={B} T={T}", flush=True)
+    plan = M.sparse_attn_sharedkv_metadata(
+        num_heads_q=64, num_heads_kv=1, head_dim=576,
+        cu_seqlens_q=torch.from_numpy(cu).cuda(), seqused_kv=torch.from_numpy(kv.astype(np.int32)).cuda(),
+        batch_size=B, max_seqlen_q=S, max_seqlen_kv=int(kv.max()), cmp_topk=K, cmp_ratio=4,
+        layout_q="TND", has_cmp_kv=True, aic_core_num=cores)
+    torch.cuda.synchronize()
+    p = plan.cpu().numpy()
+    assert p[0] == M.PLAN_MAGIC and p[2] == T
+    U, slots, unit_cap = int(p[3]), int(p[7]), int(p[11])
+    assert 0 < U <= unit_cap
+    tok = p[M.PLAN_HDR:M.PLAN_HDR + M.PLAN_TOK_W * T].reshape(T, M.PLAN_TOK_W)
+    units = p[M.PLAN_HDR + M.PLAN_TOK_W * T:][:M.PLAN_UNIT_W * unit_cap].reshape(unit_cap, M.PLAN_UNIT_W)[:U]
+    nsplit_tok = int(p[6])
+    stoks = p[M.PLAN_HDR + M.PLAN_TOK_W * T + M.PLAN_UNIT_W * unit_cap:][:nsplit_tok]
+    by_tok = {}
+    for t, r0, r1, i in units.tolist():
+        by_tok.setdefault(t, []).append((i, r0, r1))
+    used = np.zeros(slots, np.int32)
+    for b in range(B):
+        for s in range(int(act_q[b])):
+            t = int(cu[b]) + s
+            sg = int(kv[b]) - int(act_q[b]) + s
+            nwin = sg + 1 - max(sg - 127, 0)
+            ncmp = min(K, (sg + 1) // 4)
+            assert tuple(tok[t, :6]) == (b, s, sg, nwin, max(sg - 127, 0), ncmp), t
+            parts = sorted(by_tok.pop(t))
+            assert [i for i, _, _ in parts] == list(range(len(parts))) == list(range(tok[t, 6]))
+            edge = 0
+            for _, r0, r1 in parts:
+                assert r0 == edge and r1 > r0
+                edge = r1
+            assert edge == nwin + ncmp
+            if len(parts) > 1:
+                base = int(tok[t, 7])
+                used[base:base + len(parts)] += 1
+                assert t in stoks
+            else:
+                assert tok[t, 7] == -1 and t not in stoks
+    assert not by_tok, f"units for tokens no batch owns: {list(by_tok)[:5]}"
+    assert (used == 1).all(), "split workspace slots overlap or go unused"

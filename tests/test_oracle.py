@@ -347,3 +347,49 @@ def test_c_oracle_matches_numpy_oracle(kw):
     np.testing.assert_allclose(l_np, l_c, rtol=1e-5, atol=1e-5)
     # almost every element identical (summation order is the only difference)
     assert np.mean(o_np == o_c) > 0.97
+
+
+# ---------------------------------------------------------------------------
+# fp8 e4m3 (OCP e4m3fn) decoding, pinned by torch's own float8 conversion.
+# ---------------------------------------------------------------------------
+def _torch_e4m3_table():
+    import torch
+
+    return torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+
+
+def test_fp8_e4m3_decode_matches_torch_all_codes():
+    want = _torch_e4m3_table()
+    got = G.fp8e4m3_to_f32(np.arange(256, dtype=np.uint8))
+    nan = np.isnan(want)
+    assert nan.sum() == 2 and np.array_equal(np.isnan(got), nan)  # 0x7f and 0xff
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.array_equal(np.signbit(got[~nan]), np.signbit(want[~nan]))  # -0 at 0x80
+
+
+def test_c_fp8_decode_matches_torch_all_finite_codes():
+    """A single key with sink = -inf returns its V row exactly (out = V), so the
+    C oracle's dequantised row is observable: it must be torch's decoding of
+    every finite code times the row scale."""
+    from oracle import golden_c
+
+    want = _torch_e4m3_table()
+    codes = np.arange(256, dtype=np.uint8)
+    codes[np.isnan(want)] = 0
+    D = 576
+    row = np.zeros(D, np.uint8)
+    row[:256] = codes
+    row[256:512] = codes[::-1]
+    ori = np.zeros((1, 64, D), np.uint8)
+    ori[0, 0] = row
+    scale = np.zeros((1, 64), np.float32)
+    scale[0, 0] = 0.5
+    q = np.zeros((1, 1, D), np.float32)
+    out, lse = golden_c.attention(q=q, ori_kv=ori, ori_block_table=np.zeros((1, 1), np.int32),
+                                  q_prefix=[0], act_q=[1], seqused_kv=[1],
+                                  sinks=np.array([-np.inf], np.float32), softmax_scale=1.0,
+                                  scenario=1, d_v=512, q_dtype="fp32", kv_dtype="fp8e4m3",
+                                  ori_scale=scale)
+    exp = np.concatenate([want[codes], want[codes[::-1]]]) * np.float32(0.5)
+    assert np.array_equal(out[0, 0], exp.astype(np.float32))
+    assert lse[0, 0] == 0.0  # log of one key at logit 0
