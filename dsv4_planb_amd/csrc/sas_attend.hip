@@ -5,14 +5,25 @@
 // its compressed rows).  Wave w owns query heads [32 w, 32 w + 32); Q stays in
 // VGPRs (36 x 16-B fragments at d_qk = 576) and the fp32 O^T accumulator of
 // 512 x 32 fills the AGPRs.  KV rows are gathered 32 at a time (one tile) by
-// direct global -> LDS DMA (16 B per lane) into a 4-slot ring, three tiles ahead
+// buffer loads that write LDS directly, into a 4-slot ring, three tiles ahead
 // of the one being consumed.
 //
 // Per tile, per wave (32 keys x 32 heads):
-//   S^T = K Q^T      36 MFMA 32x32x16, A = K rows from LDS (ds_read_b128), B = Q
+//   S^T = K Q^T      36 MFMA 32x32x16 into a VGPR accumulator, A = K rows from LDS
+//                    (ds_read_b128, three ahead), B = Q; tile it+3's DMA is
+//                    spread over the chain
 //   softmax          P = 2^(x - m) in a per-unit frame m, bf16(P)
-//   O^T += V^T P^T   32 MFMA, A = V^T read transposed from LDS (ds_read_b64_tr_b16),
-//                    B = P^T straight from the S^T accumulator registers
+//   O^T += V^T P^T   32 MFMA into the AGPRs, A = V^T read transposed from LDS
+//                    (ds_read_b64_tr_b16, three ahead), B = P^T straight from the
+//                    S^T registers; one inline-assembly block that also carries the
+//                    scalar load of tile it+4's row addresses
+//
+// Row addresses: the resolve kernel turns each row code into a 64-bit pool
+// address (the shared zero row for -1).  Each wave gathers 8 rows per tile
+// through raw buffer resources based at those addresses, so the addresses are
+// wave-uniform (SGPRs) and nothing in the loop divides or indexes page tables.
+// Every DMA is a buffer load, never the FLAT form: an outstanding FLAT load that
+// writes LDS makes the compiler drain every later LDS wait to zero.
 //
 // Softmax (reference golden.py:156-200): the state of a head is (m, l, O) seeded
 // with (sink, 1, 0) on the unit that holds the token's first rows.  O / l and
@@ -46,9 +57,6 @@ namespace sas {
 
 constexpr float REDO_SLACK = 64.f;
 
-typedef __bf16 bf16x4_t __attribute__((__vector_size__(4 * sizeof(__bf16))));
-typedef __fp16 f16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 // Workgroup barrier without the memory fences of __syncthreads(): those wait for
@@ -59,29 +67,8 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Four 16-bit elements of one LDS column from four consecutive rows:
-// ds_read_b64_tr_b16 hands lane i of a 16-lane group element r of the 8-byte
-// chunk addressed by lane 4 r + (i >> 2) of that group, element (i & 3).
-template <int QT>
-__device__ __forceinline__ u32x2_t lds_read_tr16(const lds_u8* p) {
-  typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4;
-  typedef __attribute__((address_space(3))) f16x4_t lds_f16x4;
-  if constexpr (QT == 0) {
-    const bf16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
-    return __builtin_bit_cast(u32x2_t, v);
-  } else {
-    const f16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_f16x4*)p);
-    return __builtin_bit_cast(u32x2_t, v);
-  }
-}
-
 __device__ __forceinline__ u32x4_t lds_read_b128(const lds_u8* p) {
   return *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(p);
-}
-
-__device__ __forceinline__ void dma16(const uint8_t* src, lds_u8* dst) {
-  __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)dst,
-                                   16, 0, 0);
 }
 
 // Swizzle of the latent region: chunk c of row r sits at c ^ swz_a(r).
@@ -93,10 +80,44 @@ template <int DQK>
 struct AttendLds {
   static constexpr int TILEB = SAS_TILE * (1024 + 64) + SAS_TILE * (DQK - 512) * 2;
   uint8_t tiles[4 * TILEB];
-  const uint8_t* rowaddr[4][SAS_TILE];
-  int codes[4][SAS_TILE];  // row codes of the next tiles, fetched by DMA
-  int far;                 // a logit of some head outgrew the frame
+  int far;  // a logit of some head outgrew the frame
 };
+
+// d = a b^T + 0 / d += a b^T in VGPRs (the O accumulator owns the AGPRs).  Written as
+// inline assembly so the S accumulator is a VGPR tuple; the chain's only hazard, a
+// VALU read of d, is covered by vgpr_mfma_drain.
+template <int QT>
+__device__ __forceinline__ void vmfma_first(f32x16_t& d, const u32x4_t& a, const u32x4_t& b) {
+  if constexpr (QT == 0)
+    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  else
+    asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+}
+template <int QT>
+__device__ __forceinline__ void vmfma_acc(f32x16_t& d, const u32x4_t& a, const u32x4_t& b) {
+  if constexpr (QT == 0)
+    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  else
+    asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+}
+// An 8-pass XDL result read by a VALU needs NumPasses + 4 wait states on gfx950;
+// 24 covers it with margin.
+__device__ __forceinline__ void vgpr_mfma_drain(f32x16_t& d) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(d));
+}
+
+#define SB() __builtin_amdgcn_sched_barrier(0)
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
+// vmcnt[5:4] << 14).  Issued through the builtin so the compiler's own wait
+// insertion knows these counters are drained.
+constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | (7 << 4) | ((lgkm & 15) << 8) | (((vm >> 4) & 3) << 14);
+}
+__device__ __forceinline__ void wait_barrier() {
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+  __builtin_amdgcn_s_barrier();
+}
 
 // One work unit u.  Returns true (workgroup-uniform) when the first pass must be
 // redone; m_obs then holds each lane's observed maximum (log2 units), which the
@@ -104,11 +125,9 @@ struct AttendLds {
 template <int DQK, int QT, bool REDO>
 __device__ __forceinline__ bool attend_unit(
     int u, AttendLds<DQK>& sm, const SasFwdArgs& a, const uint16_t* __restrict__ q,
-    const uint8_t* __restrict__ ori_kv, const uint8_t* __restrict__ cmp_kv,
-    const int* __restrict__ cmp_bt, const int* __restrict__ rows_list,
-    const int* __restrict__ ncmp, const float* __restrict__ sinks, const int* __restrict__ plan,
-    uint16_t* __restrict__ out, float* __restrict__ lse, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, float& m_obs) {
+    const uint64_t* __restrict__ addr_list, const int* __restrict__ ncmp,
+    const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
+    float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml, float& m_obs) {
   constexpr int DV = 512;
   constexpr int NT = 256;
   constexpr int TILE = SAS_TILE;          // 32 keys
@@ -121,12 +140,10 @@ __device__ __forceinline__ bool attend_unit(
   constexpr int TILEA = TILE * STRA;
   constexpr int TILEB = TILEA + TILE * ROWR;
   constexpr int KSTEPS = DQK / 16;        // MFMA k-steps of Q K^T: 36 / 32
-  constexpr int CPT = TILE / 4 + (ROPE ? 1 : 0);  // DMA instructions per wave per tile
+  constexpr int CPT = 8 + (ROPE ? 8 : 0); // DMA instructions per wave per tile
   static_assert(TILE == 32, "the MFMA tiling assumes 32-key tiles");
-
   static_assert(AttendLds<DQK>::TILEB == TILEB, "LDS layout");
   lds_u8* const tiles = (lds_u8*)sm.tiles;
-  auto& rowaddr = sm.rowaddr;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -147,29 +164,17 @@ __device__ __forceinline__ bool attend_unit(
   }
 
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
-  const int b = tk[TK_B], nwin = tk[TK_NWIN];
+  const int nwin = tk[TK_NWIN];
   const int splits = tk[TK_SPLITS], wsbase = tk[TK_WSBASE];
   const int r0 = ur[1];
   const int r1 = min(ur[2], nwin + ncmp[t]);
   const int ntiles = r1 > r0 ? (r1 - r0 + TILE - 1) / TILE : 0;
-  const int* codes = rows_list + (size_t)t * a.list_stride;
-
-  // Row code of list row r (-1 = a row read as zeros): the token's list holds its
-  // window rows, then its compressed rows, contiguously.
-  auto row_code = [&](int r) -> int { return r < r1 ? codes[r] : -1; };
-  auto row_ptr = [&](int r, int code) -> const uint8_t* {
-    if (code < 0) return g_zero_row;
-    if (r < nwin) {
-      const int page = code / a.ori_block_size, off = code - page * a.ori_block_size;
-      return ori_kv + ((size_t)page * a.ori_block_stride + (size_t)off * a.ori_row_stride) * 2;
-    }
-    const int page = code / a.cmp_block_size, off = code - page * a.cmp_block_size;
-    return cmp_kv + ((size_t)page * a.cmp_block_stride + (size_t)off * a.cmp_row_stride) * 2;
-  };
+  // row addresses of this unit's list (pool addresses; -1 codes read the zero row)
+  const uint64_t* alist = addr_list + (size_t)t * a.list_stride + r0;
 
   // ---- per-lane LDS offsets (bytes within a tile) ----
   // K, latent k-step ks < 32: row li, chunk 2 ks + g -> kofs[ks & 1] + 64 (ks >> 1).
-  // K, rope k-step 32 + j: row li, rope chunk 2 j + g -> kofs_r[j].
+  // K, rope k-step 32 + j: row li, rope chunk 2 j + g -> kofs_r + 32 j (XOR folded below).
   uint32_t kofs[2], kofs_r[4];
   {
     const int f = swz_a(li);
@@ -217,172 +222,245 @@ __device__ __forceinline__ bool attend_unit(
   float m_run = REDO ? m_obs : sink2;  // redo: the frame is the maximum pass 1 observed
 
   // ---- gather: tile i goes to ring slot i & 3 ----
-  // Latent: instruction k of wave w copies row 4 k + w; lane l fetches source chunk
-  // l ^ swz_a(4 k + w) = l ^ (k & 3) into slot l.  Rope: wave w copies rows
-  // 8 w .. 8 w + 7, lane l row 8 w + (l >> 3), slot l & 7 <- chunk (l & 7) ^ swz_b(row).
+  // Wave w copies rows 8 w .. 8 w + 7 of every tile.  Latent: instruction k copies
+  // row 8 w + k, lane l fetching source chunk l ^ swz_a(8 w + k) =
+  // l ^ ((2 w + (k >> 2)) & 3) into slot l.  Row addresses reach SGPRs by scalar
+  // loads an iteration before their DMA.
   const int wu = __builtin_amdgcn_readfirstlane(w);  // the wave index as a scalar
   const uint32_t ulane = (uint32_t)lane;
-  auto dma_tile = [&](int i) {
-    const int slot = i & (NSTAGE - 1);
-    lds_u8* dstA = tiles + slot * TILEB;
-    const uint64_t mine = (uint64_t)rowaddr[slot][4 * (lane & 7) + wu];
+  const uint32_t voffA0 = 16u * (ulane ^ (uint32_t)((2 * wu) & 3));
+  const uint32_t voffA1 = 16u * (ulane ^ (uint32_t)((2 * wu + 1) & 3));
+  uint32_t voffR[4];
 #pragma unroll
-    for (int k = 0; k < TILE / 4; ++k) {
-      const uint64_t rb = ((uint64_t)__builtin_amdgcn_readlane((uint32_t)(mine >> 32), k) << 32) |
-                          (uint32_t)__builtin_amdgcn_readlane((uint32_t)mine, k);
-      const uint32_t off = 16u * (ulane ^ (uint32_t)(k & 3));
-      dma16((const uint8_t*)rb + off, dstA + (4 * k + wu) * STRA);
+  for (int j = 0; j < 4; ++j)
+    voffR[j] = (uint32_t)ROWA + 16u * ((ulane & 7u) ^ (uint32_t)((4 * wu + j) & 7));
+  typedef uint64_t RowAddrs __attribute__((ext_vector_type(8)));
+  auto fix_tail = [&](RowAddrs ra, int i) -> RowAddrs {  // rows past r1 read the zero row
+    const int rb = r0 + i * TILE + 8 * wu;
+    if (rb + 8 > r1) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (rb + k >= r1) ra[k] = (uint64_t)g_zero_row;
     }
+    return ra;
+  };
+  auto load_addrs = [&](int i) -> RowAddrs {
+    const int il = min(i, ntiles - 1);  // dead tiles (i >= ntiles) read zeros
+    return fix_tail(*reinterpret_cast<const RowAddrs*>(alist + il * TILE + 8 * wu), i);
+  };
+  // One row through a raw buffer resource based at the row (loads directly into
+  // LDS, never the FLAT form: an outstanding FLAT load that writes LDS makes every
+  // later LDS wait a full drain).
+  auto row_rsrc = [&](uint64_t addr) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)addr, (short)0, ROWA + ROWR, 0x00020000);
+  };
+  auto dma_lat = [&](int i, const RowAddrs& ra, int k) {
+    lds_u8* dst = tiles + (i & (NSTAGE - 1)) * TILEB + (8 * wu + k) * STRA;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(row_rsrc(ra[k]), (void __attribute__((address_space(3)))*)dst, 16,
+                                             k < 4 ? voffA0 : voffA1, 0, 0, 0);
+  };
+  // Rope: lanes 0..7 copy the 128-B rope of one row per instruction, chunk
+  // l ^ swz_b(8 w + k) = l ^ ((4 w + (k >> 1)) & 7) into slot l.
+  auto dma_rope = [&](int i, const RowAddrs& ra) {
     if constexpr (ROPE) {
-      const int row = 8 * wu + (lane >> 3);
-      const uint8_t* rr = rowaddr[slot][row];
-      dma16(rr + (uint32_t)(ROWA + 16 * ((lane & 7) ^ swz_b(row))), dstA + TILEA + 8 * wu * ROWR);
-    }
-  };
-
-  // Row codes of tile i reach LDS by a 4-byte DMA (wave 0, lanes < 32, slot i & 3)
-  // so that no global load with a VGPR result sits inside the tile loop: the
-  // compiler would have to drain every outstanding tile DMA to consume it.
-  auto dma_codes = [&](int i) {
-    const int r = r0 + i * TILE + lane;
-    if (lane < TILE && r < r1)
-      __builtin_amdgcn_global_load_lds((const void*)(codes + r),
-                                       (__attribute__((address_space(3))) void*)&sm.codes[i & 3][0],
-                                       4, 0, 0);
-  };
-
-  // Pipeline, per iteration it (one barrier):
-  //   wait   until tile it has landed (tiles it+1, it+2 may still be in flight)
-  //   wave 0 writes the row addresses of tile it+3 (codes DMA'd two iterations ago)
-  //   barrier: tile it visible; every wave is done with tile it-1, whose slot
-  //            (= slot of it+3) is free
-  //   DMA    codes of tile it+5 (wave 0), then tile it+3 (all waves)
-  //   compute S, softmax and PV of tile it
-  // prologue: row addresses of tiles 0..2, codes of tiles 3 and 4, DMA of tiles 0..2
-  if (!REDO && tid == 0) sm.far = 0;
-  if (tid < 3 * TILE) {
-    const int r = r0 + tid;  // tile tid / 32, row tid % 32
-    rowaddr[tid / TILE][tid % TILE] = row_ptr(r, row_code(r));
-  }
-  lds_barrier();
-  if (wu == 0) {
-    if (ntiles > 3) dma_codes(3);
-    if (ntiles > 4) dma_codes(4);
-  }
-  if (ntiles > 0) dma_tile(0);
-  if (ntiles > 1) dma_tile(1);
-  if (ntiles > 2) dma_tile(2);
-
-  // O^T += V^T P^T for one tile
-  auto pv = [&](const lds_u8* tl, const u32x4_t(&pk)[2]) {
+      lds_u8* dst = tiles + (i & (NSTAGE - 1)) * TILEB + TILEA + 8 * wu * ROWR;
+      if (lane < 8) {
 #pragma unroll
-    for (int mb = 0; mb < 16; ++mb) {
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const lds_u8* p = tl + 64 * mb + 16 * STRA * kk;
-        const u32x2_t lo = lds_read_tr16<QT>(p + vofs[0]);
-        const u32x2_t hi = lds_read_tr16<QT>(p + vofs[1]);
-        const u32x4_t av = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
-        acc[mb] = mfma32<QT>(av, pk[kk], acc[mb]);
+        for (int k = 0; k < 8; ++k)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(row_rsrc(ra[k]), (void __attribute__((address_space(3)))*)(dst + k * ROWR), 16,
+                                                   voffR[k >> 1], 0, 0, 0);
       }
     }
-    // operand reads run one MFMA ahead of their MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-    for (int i = 0; i < 31; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
   };
 
-  // Per-lane partial sums over this lane's keys (the two half-waves of a head see
-  // different keys); they are combined once, after the loop.
-  float pe = 0.f;          // sum of P (LSE)
+  // ---- S^T = K Q^T: K fragments three ahead, tile it+3's DMA spread over the chain ----
+  auto kread = [&](const lds_u8* tl, int ks) -> u32x4_t {
+    return ks < 32 ? lds_read_b128(tl + kofs[ks & 1] + 64 * (ks >> 1))
+                   : lds_read_b128(tl + kofs_r[(ks - 32) & 3]);
+  };
+  auto qk = [&](const lds_u8* tl, int inext, const RowAddrs& ra) -> f32x16_t {
+    u32x4_t kb[3];
+    kb[0] = kread(tl, 0);
+    kb[1] = kread(tl, 1);
+    kb[2] = kread(tl, 2);
+    SB();
+    f32x16_t s;
+    vmfma_first<QT>(s, kb[0], qf[0]);
+    SB();
+#pragma unroll
+    for (int ks = 1; ks < KSTEPS; ++ks) {
+      if (ks + 2 < KSTEPS) kb[(ks + 2) % 3] = kread(tl, ks + 2);
+      vmfma_acc<QT>(s, kb[ks % 3], qf[ks]);
+      if ((ks & 3) == 1 && (ks >> 2) < 8) dma_lat(inext, ra, ks >> 2);
+      if (ks == 33) dma_rope(inext, ra);
+      SB();
+    }
+    vgpr_mfma_drain(s);
+    return s;
+  };
+
+  // ---- O^T += V^T P^T ----
+  // PV in one inline-assembly block that also carries the scalar load of a later
+  // tile's row addresses: its latency hides under the 32 MFMAs, and the block's
+  // own LDS waits count only the V^T reads (a scalar load in flight can only make
+  // them stricter), so the loaded SGPRs are valid when the block ends.
+  // V^T operand ring: three 4-VGPR buffers v[244:255] (clobbered), reads 3 MFMAs ahead.
+  auto pv_asm = [&](const lds_u8* tl, const u32x4_t(&pk)[2], const uint64_t* aptr) -> RowAddrs {
+    const uint32_t a0 = (uint32_t)(uintptr_t)tl + vofs[0];
+    const uint32_t a1 = (uint32_t)(uintptr_t)tl + vofs[1];
+    typedef uint32_t u32x16_t __attribute__((ext_vector_type(16)));
+    u32x16_t sa;
+#define PV_RD(j, b) \
+    "ds_read_b64_tr_b16 v[" #b ":" #b "+1], %[a0] offset:" #j "\n\t" \
+    "ds_read_b64_tr_b16 v[" #b "+2:" #b "+3], %[a1] offset:" #j "\n\t"
+#define PV_MM(MN, c, b, p) MN " %[c" #c "], v[" #b ":" #b "+3], %[p" #p "], %[c" #c "]\n\t"
+#define PV_ASM(MN) \
+    asm volatile( \
+        "s_load_dwordx16 %[sa], %[ap], 0x0\n\t" \
+        PV_RD(0, 244) PV_RD(17408, 248) PV_RD(64, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 0, 244, 0) PV_RD(17472, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 0, 248, 1) PV_RD(128, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 1, 252, 0) PV_RD(17536, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 1, 244, 1) PV_RD(192, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 2, 248, 0) PV_RD(17600, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 2, 252, 1) PV_RD(256, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 3, 244, 0) PV_RD(17664, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 3, 248, 1) PV_RD(320, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 4, 252, 0) PV_RD(17728, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 4, 244, 1) PV_RD(384, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 5, 248, 0) PV_RD(17792, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 5, 252, 1) PV_RD(448, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 6, 244, 0) PV_RD(17856, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 6, 248, 1) PV_RD(512, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 7, 252, 0) PV_RD(17920, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 7, 244, 1) PV_RD(576, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 8, 248, 0) PV_RD(17984, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 8, 252, 1) PV_RD(640, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 9, 244, 0) PV_RD(18048, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 9, 248, 1) PV_RD(704, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 10, 252, 0) PV_RD(18112, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 10, 244, 1) PV_RD(768, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 11, 248, 0) PV_RD(18176, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 11, 252, 1) PV_RD(832, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 12, 244, 0) PV_RD(18240, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 12, 248, 1) PV_RD(896, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 13, 252, 0) PV_RD(18304, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 13, 244, 1) PV_RD(960, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 14, 248, 0) PV_RD(18368, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 14, 252, 1) \
+        "s_waitcnt lgkmcnt(2)\n\t" PV_MM(MN, 15, 244, 0) \
+        "s_waitcnt lgkmcnt(0)\n\t" PV_MM(MN, 15, 248, 1) \
+        : [sa] "=s"(sa), [c0] "+a"(acc[0]), [c1] "+a"(acc[1]), [c2] "+a"(acc[2]), [c3] "+a"(acc[3]), \
+          [c4] "+a"(acc[4]), [c5] "+a"(acc[5]), [c6] "+a"(acc[6]), [c7] "+a"(acc[7]), \
+          [c8] "+a"(acc[8]), [c9] "+a"(acc[9]), [c10] "+a"(acc[10]), [c11] "+a"(acc[11]), \
+          [c12] "+a"(acc[12]), [c13] "+a"(acc[13]), [c14] "+a"(acc[14]), [c15] "+a"(acc[15]) \
+        : [a0] "v"(a0), [a1] "v"(a1), [p0] "v"(pk[0]), [p1] "v"(pk[1]), [ap] "s"(aptr) \
+        : "v244", "v245", "v246", "v247", "v248", "v249", "v250", "v251", "v252", "v253", \
+          "v254", "v255", "memory");
+    if constexpr (QT == 0) {
+      PV_ASM("v_mfma_f32_32x32x16_bf16")
+    } else {
+      PV_ASM("v_mfma_f32_32x32x16_f16")
+    }
+#undef PV_ASM
+#undef PV_RD
+#undef PV_MM
+    return __builtin_bit_cast(RowAddrs, sa);
+  };
+
+  // ---- softmax of one tile: P = 2^(S c - m) rounded to bf16, sums ----
+  float pe = 0.f;          // sum of P (LSE), per lane
   float pw = 0.f;          // sum of bf16(P): what entered PV (output normaliser)
   float xobs = -INFINITY;  // max of x - m over the unit, for the overflow guard
   const float c = a.scale_log2;
-  for (int it = 0; it < ntiles; ++it) {
-    // tile it has landed (this wave's share): the tile DMAs issued after it (at most
-    // two) may still be pending; wave 0's code DMAs were issued before those, so
-    // the same count also completes the codes of tile it+3
-    if (it + 2 < ntiles)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * CPT) : "memory");
-    else if (it + 1 < ntiles)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CPT) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (wu == 0 && it + 3 < ntiles && lane < TILE) {
-      const int r3 = r0 + (it + 3) * TILE + lane;
-      rowaddr[(it + 3) & (NSTAGE - 1)][lane] =
-          row_ptr(r3, r3 < r1 ? sm.codes[(it + 3) & 3][lane] : -1);
-    }
-    lds_barrier();
-    if (wu == 0 && it + 5 < ntiles) dma_codes(it + 5);  // before the tile DMA (vmcnt order)
-    if (it + 3 < ntiles) dma_tile(it + 3);
-
-    const lds_u8* tl = tiles + (it & (NSTAGE - 1)) * TILEB;
-    // ---- S^T = K Q^T (each K fragment is read one MFMA ahead) ----
-    auto kread = [&](int ks) -> u32x4_t {
-      return ks < 32 ? lds_read_b128(tl + kofs[ks & 1] + 64 * (ks >> 1))
-                     : lds_read_b128(tl + kofs_r[(ks - 32) & 3]);
-    };
-    f32x16_t s = f32x16_t{};
-    u32x4_t kcur = kread(0);
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      const u32x4_t knext = ks + 1 < KSTEPS ? kread(ks + 1) : kcur;
-      s = mfma32<QT>(kcur, qf[ks], s);
-      kcur = knext;
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-    for (int i = 0; i < KSTEPS - 1; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read, one ahead
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-
-    // ---- softmax ----
-    // x = S c - m (log2 units); the first tile of the first pass fixes the frame m.
-    const bool first = !REDO && it == 0;
+  auto softmax = [&](f32x16_t s, u32x4_t(&pk)[2], bool first, int nvalid) {
     float x[16];
+    if (first) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] = first ? s[r] * c : fmaf(s[r], c, -m_run);
-    const int nvalid = r1 - (r0 + it * TILE);
-    if (__builtin_expect(nvalid < TILE, 0)) {  // the unit's last tile: rows past r1
+      for (int r = 0; r < 16; ++r) x[r] = s[r] * c;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = fmaf(s[r], c, -m_run);
+    }
+    if (nvalid < TILE) {  // the unit's last tile: rows past r1
       const int lim = nvalid - 4 * g;
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (8 * (r >> 2) + (r & 3) >= lim) x[r] = -INFINITY;
     }
-    if (first) {  // O is still zero: no rescale needed
-      float mt = x[0];
+    if (first) {  // O is still zero: the first tile fixes the frame
+      float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mt = fmaxf(mt, x[r]);
+      for (int r = 4; r < 16; r += 2) mt = fmaxf(mt, fmaxf(x[r], x[r + 1]));
       m_run = fmaxf(m_run, fmaxf(mt, __shfl_xor(mt, 32)));
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] -= m_run;
     }
-    float xm = x[0];
+    float xm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
 #pragma unroll
-    for (int r = 1; r < 16; ++r) xm = fmaxf(xm, x[r]);
+    for (int r = 4; r < 16; r += 2) xm = fmaxf(xm, fmaxf(x[r], x[r + 1]));
     xobs = fmaxf(xobs, xm);
-    u32x4_t pk[2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      x[r] = __builtin_amdgcn_exp2f(x[r]);  // 2^x; below 2^-126 of the frame flushes to 0
-      pe += x[r];
-    }
+    for (int r = 0; r < 16; ++r) x[r] = __builtin_amdgcn_exp2f(x[r]);  // 2^x, underflow -> 0
+    float t8[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) t8[r] = x[2 * r] + x[2 * r + 1];
+    pe += ((t8[0] + t8[1]) + (t8[2] + t8[3])) + ((t8[4] + t8[5]) + (t8[6] + t8[7]));
+    float w2[2] = {0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         pk[kk][e] = pack2_q16<QT>(x[8 * kk + 2 * e], x[8 * kk + 2 * e + 1]);
-        pw = sum2_q16<QT>(pk[kk][e], pw);
+        w2[e & 1] = sum2_q16<QT>(pk[kk][e], w2[e & 1]);
       }
-    // ---- O^T += V^T P^T ----
-    pv(tl, pk);
+    pw += w2[0] + w2[1];
+  };
+
+
+  if (!REDO && tid == 0) sm.far = 0;
+  if (ntiles > 0) {
+    // prologue: tiles 0..2 in flight, addresses of tile 3 in SGPRs
+    RowAddrs ra_next = load_addrs(0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dma_lat(0, ra_next, k);
+    dma_rope(0, ra_next);
+    ra_next = load_addrs(1);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dma_lat(1, ra_next, k);
+    dma_rope(1, ra_next);
+    ra_next = load_addrs(2);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dma_lat(2, ra_next, k);
+    dma_rope(2, ra_next);
+    ra_next = load_addrs(3);
+
+    // One tile: wait for it (the two younger tiles' DMAs may still be in flight),
+    // barrier (tile visible; every wave is done with tile it-1, whose slot tile
+    // it+3 reuses), S with tile it+3's DMA interleaved, softmax, PV, then the
+    // scalar loads of tile it+4's row addresses (after this tile's LDS reads, so
+    // the LDS waits above count exactly; the next barrier's lgkmcnt(0) covers them).
+    auto tile = [&](int it, bool first, bool edge) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * CPT, 15));
+      wait_barrier();
+      const RowAddrs ra_cur = ra_next;
+      const lds_u8* tl = tiles + (it & (NSTAGE - 1)) * TILEB;
+      const f32x16_t s = qk(tl, it + 3, ra_cur);
+      u32x4_t pk[2];
+      softmax(s, pk, first, edge ? r1 - (r0 + it * TILE) : TILE);
+      SB();
+      {
+        const int il = min(it + 4, ntiles - 1);  // dead tiles (>= ntiles) read zeros
+        ra_next = fix_tail(pv_asm(tl, pk, alist + il * TILE + 8 * wu), it + 4);
+      }
+    };
+    tile(0, !REDO, true);
+    for (int it = 1; it + 1 < ntiles; ++it) tile(it, false, false);
+    if (ntiles > 1) tile(ntiles - 1, false, true);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the dead-tile DMAs have landed
+    // the last PV MFMAs (inline assembly) write the accumulators: wait out the
+    // XDL-write -> VALU-read hazard before the epilogue reads them
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   }
   pe += __shfl_xor(pe, 32);
   pw += __shfl_xor(pw, 32);
@@ -449,18 +527,18 @@ template <int DQK, int QT>
 __global__ __launch_bounds__(256, 1) void attend_kernel(
     SasFwdArgs a, const uint16_t* __restrict__ q, const uint8_t* __restrict__ ori_kv,
     const uint8_t* __restrict__ cmp_kv, const int* __restrict__ cmp_bt,
-    const int* __restrict__ rows_list, const int* __restrict__ ncmp,
+    const uint64_t* __restrict__ addr_list, const int* __restrict__ ncmp,
     const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
     float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   __shared__ __attribute__((aligned(16))) AttendLds<DQK> sm;
   const int u = blockIdx.x;
   if (plan[PH_MAGIC] != SAS_PLAN_MAGIC || u >= plan[PH_UNITS]) return;
   float m_obs = 0.f;
-  if (attend_unit<DQK, QT, false>(u, sm, a, q, ori_kv, cmp_kv, cmp_bt, rows_list, ncmp, sinks,
-                                  plan, out, lse, ws_o, ws_ml, m_obs)) {
+  if (attend_unit<DQK, QT, false>(u, sm, a, q, addr_list, ncmp, sinks, plan, out, lse, ws_o,
+                                  ws_ml, m_obs)) {
     lds_barrier();  // every wave is done with the ring before the redo refills it
-    attend_unit<DQK, QT, true>(u, sm, a, q, ori_kv, cmp_kv, cmp_bt, rows_list, ncmp, sinks, plan,
-                               out, lse, ws_o, ws_ml, m_obs);
+    attend_unit<DQK, QT, true>(u, sm, a, q, addr_list, ncmp, sinks, plan, out, lse, ws_o, ws_ml,
+                               m_obs);
   }
 }
 

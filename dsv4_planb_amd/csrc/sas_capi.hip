@@ -97,6 +97,7 @@ int check_tensors(const sas_params_t* p, const sas_tensors_t* t) {
 
 struct Ws {
   int* rows;
+  uint64_t* addr;
   int* ncmp;
   int* plan;
   float* o;
@@ -111,6 +112,7 @@ int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out)
   if (((uintptr_t)ws & 255u) != 0) return SAS_ERR_WORKSPACE;
   char* base = static_cast<char*>(ws);
   out->rows = reinterpret_cast<int*>(base + W.off_rows);
+  out->addr = reinterpret_cast<uint64_t*>(base + W.off_addr);
   out->ncmp = reinterpret_cast<int*>(base + W.off_ncmp);
   out->plan = reinterpret_cast<int*>(base + W.off_plan);
   out->o = reinterpret_cast<float*>(base + W.off_o);
@@ -148,7 +150,7 @@ fwd_fn_t pick_fwd(const sas_params_t* p) {
 }
 
 typedef void (*attend_fn_t)(SasFwdArgs, const uint16_t*, const uint8_t*, const uint8_t*,
-                            const int*, const int*, const int*, const float*, const int*,
+                            const int*, const uint64_t*, const int*, const float*, const int*,
                             uint16_t*, float*, float*, float*);
 
 attend_fn_t pick_attend(const sas_params_t* p) {
@@ -269,7 +271,9 @@ int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   if (p->total_tokens == 0) return SAS_OK;
   hipLaunchKernelGGL(sas::resolve_kernel, dim3(p->total_tokens), dim3(sas::RS_NT), 0,
                      (hipStream_t)stream, fwd_args(p, target), plan, t->ori_block_table,
-                     t->cmp_sparse_indices, t->cmp_block_table, w.rows, w.ncmp);
+                     t->cmp_sparse_indices, t->cmp_block_table, w.rows, w.ncmp, w.addr,
+                     static_cast<const uint8_t*>(t->ori_kv), static_cast<const uint8_t*>(t->cmp_kv),
+                     p->kv_dtype == SAS_DT_FP8E4M3 ? 1 : 2);
   return launch_status();
 }
 
@@ -287,7 +291,7 @@ int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pla
   if (p->kv_dtype != SAS_DT_FP8E4M3) {
     hipLaunchKernelGGL(pick_attend(p), dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream, a,
                        static_cast<const uint16_t*>(t->q), static_cast<const uint8_t*>(t->ori_kv),
-                       static_cast<const uint8_t*>(t->cmp_kv), t->cmp_block_table, w.rows,
+                       static_cast<const uint8_t*>(t->cmp_kv), t->cmp_block_table, w.addr,
                        w.ncmp, t->sinks, plan, static_cast<uint16_t*>(t->out), t->lse, w.o, w.ml);
     return launch_status();
   }
@@ -399,3 +403,4 @@ int sas_graph_destroy(void* graph_exec) {
 }
 
 }  // extern "C"
+

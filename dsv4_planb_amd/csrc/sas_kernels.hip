@@ -202,6 +202,17 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
 // (page * block_size + offset) or -1 for a row the reference reads as zeros
 // (unused page).  Window codes index the raw pool, later codes the compressed pool.
 // ===========================================================================
+// The row every -1 code reads (zeros).
+__device__ __attribute__((aligned(16))) uint8_t g_zero_row[1152] = {};
+
+// Pool address of a row code (-1: the shared zero row).
+__device__ __forceinline__ uint64_t code_addr(int code, const uint8_t* pool, int block_size,
+                                              int64_t block_stride, int64_t row_stride, int esz) {
+  if (code < 0) return (uint64_t)g_zero_row;
+  const int page = code / block_size, off = code - page * block_size;
+  return (uint64_t)(pool + ((size_t)page * block_stride + (size_t)off * row_stride) * esz);
+}
+
 __device__ __forceinline__ int paged_code(const int* __restrict__ bt_row, int table_len,
                                           int block_size, int block_num, int pos) {
   const int blk = pos / block_size;
@@ -220,7 +231,11 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
                                                         const int* __restrict__ idx,
                                                         const int* __restrict__ cmp_bt,
                                                         int* __restrict__ rows_out,
-                                                        int* __restrict__ ncmp_out) {
+                                                        int* __restrict__ ncmp_out,
+                                                        uint64_t* __restrict__ addr_out,
+                                                        const uint8_t* __restrict__ ori_kv,
+                                                        const uint8_t* __restrict__ cmp_kv,
+                                                        int esz) {
   __shared__ int s_term;
   __shared__ int s_wsum[RS_NT / 64];
   const int t = blockIdx.x;
@@ -233,10 +248,15 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     return;
   }
   int* out = rows_out + (size_t)t * a.list_stride;
+  uint64_t* aout = addr_out + (size_t)t * a.list_stride;
   const int nwin = tk[TK_NWIN], winlo = tk[TK_WINLO];
   const int* obt = ori_bt + (size_t)b * a.ori_table_len;
-  for (int r = tid; r < nwin; r += RS_NT)
-    out[r] = paged_code(obt, a.ori_table_len, a.ori_block_size, a.ori_block_num, winlo + r);
+  for (int r = tid; r < nwin; r += RS_NT) {
+    const int code = paged_code(obt, a.ori_table_len, a.ori_block_size, a.ori_block_num, winlo + r);
+    out[r] = code;
+    aout[r] = code_addr(code, ori_kv, a.ori_block_size, a.ori_block_stride, a.ori_row_stride, esz);
+  }
+  aout += nwin;
   if (a.scenario == 1) {
     if (tid == 0) ncmp_out[t] = 0;
     return;
@@ -246,8 +266,11 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
   if (a.scenario == 2) {  // golden.py:146-150: every compressed row below thr
     const int n = max(min(thr, a.K), 0);
     const int* cbt2 = cmp_bt + (size_t)b * a.cmp_table_len;
-    for (int j = tid; j < n; j += RS_NT)
-      out[j] = paged_code(cbt2, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, j);
+    for (int j = tid; j < n; j += RS_NT) {
+      const int code = paged_code(cbt2, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, j);
+      out[j] = code;
+      aout[j] = code_addr(code, cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
+    }
     if (tid == 0) ncmp_out[t] = n;
     return;
   }
@@ -284,8 +307,11 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
   const int* cbt = cmp_bt + (size_t)b * a.cmp_table_len;
   for (int i = s0; i < min(s1, term); ++i) {
     const int id = ir[i];
-    if (id >= 0 && id < thr)
-      out[base++] = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, id);
+    if (id >= 0 && id < thr) {
+      const int code = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, id);
+      out[base] = code;
+      aout[base++] = code_addr(code, cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
+    }
   }
   if (tid == RS_NT - 1) {
     int total = 0;
@@ -371,7 +397,7 @@ __device__ __forceinline__ uint32_t fp8_to_q16(uint32_t v) {
 }
 
 // Source of rows that read as zeros (unused pages, tile padding).
-__device__ __attribute__((aligned(16))) uint8_t g_zero_row[1152];
+
 
 // Online softmax (golden.py:184-196): m_run is the running maximum of the sink
 // and every logit seen so far; a tile whose maximum exceeds it rescales O and l
