@@ -89,16 +89,16 @@ struct AttendLds {
 template <int QT>
 __device__ __forceinline__ void vmfma_first(f32x16_t& d, const u32x4_t& a, const u32x4_t& b) {
   if constexpr (QT == 0)
-    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
   else
-    asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
 }
 template <int QT>
 __device__ __forceinline__ void vmfma_acc(f32x16_t& d, const u32x4_t& a, const u32x4_t& b) {
   if constexpr (QT == 0)
-    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
   else
-    asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
 }
 // An 8-pass XDL result read by a VALU needs NumPasses + 4 wait states on gfx950;
 // 24 covers it with margin.
@@ -174,15 +174,14 @@ __device__ __forceinline__ bool attend_unit(
 
   // ---- per-lane LDS offsets (bytes within a tile) ----
   // K, latent k-step ks < 32: row li, chunk 2 ks + g -> kofs[ks & 1] + 64 (ks >> 1).
-  // K, rope k-step 32 + j: row li, rope chunk 2 j + g -> kofs_r + 32 j (XOR folded below).
-  uint32_t kofs[2], kofs_r[4];
+  // K, rope k-step 32 + j: row li, rope chunk 2 j + g -> kofs_r ^ 32 j (the row
+  // offset TILEA + 128 li has clear bits 4..6, which carry the swizzled chunk).
+  uint32_t kofs[2], kofs_r;
   {
     const int f = swz_a(li);
 #pragma unroll
     for (int j = 0; j < 2; ++j) kofs[j] = li * STRA + 16 * ((2 * j + g) ^ f);
-    const int fr = swz_b(li);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) kofs_r[j] = TILEA + li * ROWR + 16 * ((2 * j + g) ^ fr);
+    kofs_r = TILEA + li * ROWR + 16 * (g ^ swz_b(li));
   }
   // V^T (A of O^T += V^T P^T).  MFMA row m of d-block mb is d = 32 mb + dmap(m) with
   // dmap(m) = 16 ((m >> 2) & 1) + 4 (m >> 3) + (m & 3), so accumulator register r of
@@ -230,10 +229,8 @@ __device__ __forceinline__ bool attend_unit(
   const uint32_t ulane = (uint32_t)lane;
   const uint32_t voffA0 = 16u * (ulane ^ (uint32_t)((2 * wu) & 3));
   const uint32_t voffA1 = 16u * (ulane ^ (uint32_t)((2 * wu + 1) & 3));
-  uint32_t voffR[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    voffR[j] = (uint32_t)ROWA + 16u * ((ulane & 7u) ^ (uint32_t)((4 * wu + j) & 7));
+  // rope DMA of row 8 w + k: lane l fetches chunk l ^ ((4 w + (k >> 1)) & 7)
+  const uint32_t voffR0 = 16u * (ulane & 7u);
   typedef uint64_t RowAddrs __attribute__((ext_vector_type(8)));
   auto fix_tail = [&](RowAddrs ra, int i) -> RowAddrs {  // rows past r1 read the zero row
     const int rb = r0 + i * TILE + 8 * wu;
@@ -260,43 +257,68 @@ __device__ __forceinline__ bool attend_unit(
                                              k < 4 ? voffA0 : voffA1, 0, 0, 0);
   };
   // Rope: lanes 0..7 copy the 128-B rope of one row per instruction, chunk
-  // l ^ swz_b(8 w + k) = l ^ ((4 w + (k >> 1)) & 7) into slot l.
+  // l ^ swz_b(8 w + k) = l ^ ((4 w + (k >> 1)) & 7) into slot l.  It runs after every
+  // other use of the row addresses in its block: a uniform value used on both
+  // sides of the divergent lane < 8 branch can end up in VGPRs.
   auto dma_rope = [&](int i, const RowAddrs& ra) {
     if constexpr (ROPE) {
       lds_u8* dst = tiles + (i & (NSTAGE - 1)) * TILEB + TILEA + 8 * wu * ROWR;
       if (lane < 8) {
+        // formed here rather than kept across the loop: registers are the limit
+        uint32_t vb = voffR0;
+        asm volatile("" : "+v"(vb));
 #pragma unroll
         for (int k = 0; k < 8; ++k)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(row_rsrc(ra[k]), (void __attribute__((address_space(3)))*)(dst + k * ROWR), 16,
-                                                   voffR[k >> 1], 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              row_rsrc(ra[k]), (void __attribute__((address_space(3)))*)(dst + k * ROWR), 16,
+              ROWA + (vb ^ (16u * (uint32_t)((4 * wu + (k >> 1)) & 7))), 0, 0, 0);
       }
     }
   };
 
-  // ---- S^T = K Q^T: K fragments three ahead, tile it+3's DMA spread over the chain ----
-  auto kread = [&](const lds_u8* tl, int ks) -> u32x4_t {
+  // ---- S^T = K Q^T: the chain of KSTEPS accumulating MFMAs, K fragments three ahead ----
+  // work(ks) runs right after step ks's MFMA issues (ks = -1: before the first one,
+  // while the first K fragments are in flight).  The loop hangs the previous tile's
+  // softmax and a later tile's DMA on it, so that VALU, SALU and DMA issue overlap
+  // the matrix core instead of following it.
+  auto kread = [&](const lds_u8* tl, int ks, uint32_t kr) -> u32x4_t {
     return ks < 32 ? lds_read_b128(tl + kofs[ks & 1] + 64 * (ks >> 1))
-                   : lds_read_b128(tl + kofs_r[(ks - 32) & 3]);
+                   : lds_read_b128(tl + (kr ^ (32u * (uint32_t)(ks - 32))));
   };
-  auto qk = [&](const lds_u8* tl, int inext, const RowAddrs& ra) -> f32x16_t {
+  // Even and odd k-steps accumulate into sa and sb: an MFMA that accumulates into
+  // the previous one's result waits for it (44 instead of 32 cycles), so the chain
+  // alternates between two accumulators; S = sa + sb.
+  auto qk = [&](const lds_u8* tl, f32x16_t& sa, f32x16_t& sb, auto&& work) {
+    // the rope offset, formed per chain rather than kept across the loop
+    uint32_t kr = kofs_r;
+    asm volatile("" : "+v"(kr));
     u32x4_t kb[3];
-    kb[0] = kread(tl, 0);
-    kb[1] = kread(tl, 1);
-    kb[2] = kread(tl, 2);
+    kb[0] = kread(tl, 0, kr);
+    kb[1] = kread(tl, 1, kr);
+    kb[2] = kread(tl, 2, kr);
     SB();
-    f32x16_t s;
-    vmfma_first<QT>(s, kb[0], qf[0]);
+    work(-1);
+    SB();
+    vmfma_first<QT>(sa, kb[0], qf[0]);
+    work(0);
+    SB();
+    kb[0] = kread(tl, 3, kr);
+    vmfma_first<QT>(sb, kb[1], qf[1]);
+    work(1);
     SB();
 #pragma unroll
-    for (int ks = 1; ks < KSTEPS; ++ks) {
-      if (ks + 2 < KSTEPS) kb[(ks + 2) % 3] = kread(tl, ks + 2);
-      vmfma_acc<QT>(s, kb[ks % 3], qf[ks]);
-      if ((ks & 3) == 1 && (ks >> 2) < 8) dma_lat(inext, ra, ks >> 2);
-      if (ks == 33) dma_rope(inext, ra);
+    for (int ks = 2; ks < KSTEPS; ++ks) {
+      if (ks + 2 < KSTEPS) kb[(ks + 2) % 3] = kread(tl, ks + 2, kr);
+      vmfma_acc<QT>((ks & 1) ? sb : sa, kb[ks % 3], qf[ks]);
+      work(ks);
       SB();
     }
-    vgpr_mfma_drain(s);
-    return s;
+  };
+  // Tile i's DMA over a QK chain: one latent row every fourth step, the rope rows
+  // (behind a lane < 8 branch) after the last MFMA.
+  auto dma_step = [&](int ks, int i, const RowAddrs& ra) {
+    if (ks >= 0 && (ks & 3) == 1 && (ks >> 2) < 8) dma_lat(i, ra, ks >> 2);
+    if (ks == KSTEPS - 1) dma_rope(i, ra);
   };
 
   // ---- O^T += V^T P^T ----
@@ -305,6 +327,9 @@ __device__ __forceinline__ bool attend_unit(
   // own LDS waits count only the V^T reads (a scalar load in flight can only make
   // them stricter), so the loaded SGPRs are valid when the block ends.
   // V^T operand ring: three 4-VGPR buffers v[244:255] (clobbered), reads 3 MFMAs ahead.
+  // The MFMAs run accumulator-outer (all 16 d-blocks of key half 0, then of half 1):
+  // an MFMA that accumulates into the previous one's result waits for it (44
+  // instead of 32 cycles on gfx950), so no two consecutive MFMAs share one.
   auto pv_asm = [&](const lds_u8* tl, const u32x4_t(&pk)[2], const uint64_t* aptr) -> RowAddrs {
     const uint32_t a0 = (uint32_t)(uintptr_t)tl + vofs[0];
     const uint32_t a1 = (uint32_t)(uintptr_t)tl + vofs[1];
@@ -317,38 +342,38 @@ __device__ __forceinline__ bool attend_unit(
 #define PV_ASM(MN) \
     asm volatile( \
         "s_load_dwordx16 %[sa], %[ap], 0x0\n\t" \
-        PV_RD(0, 244) PV_RD(17408, 248) PV_RD(64, 252) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 0, 244, 0) PV_RD(17472, 244) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 0, 248, 1) PV_RD(128, 248) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 1, 252, 0) PV_RD(17536, 252) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 1, 244, 1) PV_RD(192, 244) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 2, 248, 0) PV_RD(17600, 248) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 2, 252, 1) PV_RD(256, 252) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 3, 244, 0) PV_RD(17664, 244) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 3, 248, 1) PV_RD(320, 248) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 4, 252, 0) PV_RD(17728, 252) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 4, 244, 1) PV_RD(384, 244) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 5, 248, 0) PV_RD(17792, 248) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 5, 252, 1) PV_RD(448, 252) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 6, 244, 0) PV_RD(17856, 244) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 6, 248, 1) PV_RD(512, 248) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 7, 252, 0) PV_RD(17920, 252) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 7, 244, 1) PV_RD(576, 244) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 8, 248, 0) PV_RD(17984, 248) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 8, 252, 1) PV_RD(640, 252) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 9, 244, 0) PV_RD(18048, 244) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 9, 248, 1) PV_RD(704, 248) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 10, 252, 0) PV_RD(18112, 252) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 10, 244, 1) PV_RD(768, 244) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 11, 248, 0) PV_RD(18176, 248) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 11, 252, 1) PV_RD(832, 252) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 12, 244, 0) PV_RD(18240, 244) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 12, 248, 1) PV_RD(896, 248) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 13, 252, 0) PV_RD(18304, 252) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 13, 244, 1) PV_RD(960, 244) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 14, 248, 0) PV_RD(18368, 248) \
-        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 14, 252, 1) \
-        "s_waitcnt lgkmcnt(2)\n\t" PV_MM(MN, 15, 244, 0) \
+        PV_RD(0, 244) PV_RD(64, 248) PV_RD(128, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 0, 244, 0) PV_RD(192, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 1, 248, 0) PV_RD(256, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 2, 252, 0) PV_RD(320, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 3, 244, 0) PV_RD(384, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 4, 248, 0) PV_RD(448, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 5, 252, 0) PV_RD(512, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 6, 244, 0) PV_RD(576, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 7, 248, 0) PV_RD(640, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 8, 252, 0) PV_RD(704, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 9, 244, 0) PV_RD(768, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 10, 248, 0) PV_RD(832, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 11, 252, 0) PV_RD(896, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 12, 244, 0) PV_RD(960, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 13, 248, 0) PV_RD(17408, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 14, 252, 0) PV_RD(17472, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 15, 244, 0) PV_RD(17536, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 0, 248, 1) PV_RD(17600, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 1, 252, 1) PV_RD(17664, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 2, 244, 1) PV_RD(17728, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 3, 248, 1) PV_RD(17792, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 4, 252, 1) PV_RD(17856, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 5, 244, 1) PV_RD(17920, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 6, 248, 1) PV_RD(17984, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 7, 252, 1) PV_RD(18048, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 8, 244, 1) PV_RD(18112, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 9, 248, 1) PV_RD(18176, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 10, 252, 1) PV_RD(18240, 252) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 11, 244, 1) PV_RD(18304, 244) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 12, 248, 1) PV_RD(18368, 248) \
+        "s_waitcnt lgkmcnt(4)\n\t" PV_MM(MN, 13, 252, 1) \
+        "s_waitcnt lgkmcnt(2)\n\t" PV_MM(MN, 14, 244, 1) \
         "s_waitcnt lgkmcnt(0)\n\t" PV_MM(MN, 15, 248, 1) \
         : [sa] "=s"(sa), [c0] "+a"(acc[0]), [c1] "+a"(acc[1]), [c2] "+a"(acc[2]), [c3] "+a"(acc[3]), \
           [c4] "+a"(acc[4]), [c5] "+a"(acc[5]), [c6] "+a"(acc[6]), [c7] "+a"(acc[7]), \
@@ -371,56 +396,113 @@ __device__ __forceinline__ bool attend_unit(
   // ---- softmax of one tile: P = 2^(S c - m) rounded to bf16, sums ----
   float pe = 0.f;          // sum of P (LSE), per lane
   float pw = 0.f;          // sum of bf16(P): what entered PV (output normaliser)
-  float xobs = -INFINITY;  // max of x - m over the unit, for the overflow guard
+  float xo = -INFINITY;    // max of x - m over the unit, for the overflow guard
   const float c = a.scale_log2;
-  auto softmax = [&](f32x16_t s, u32x4_t(&pk)[2], bool first, int nvalid) {
-    float x[16];
-    if (first) {
+  // The max over the tile of both half-waves (lane l and lane l ^ 32 hold the two
+  // halves of a head's 32 keys).
+  auto tile_max = [&](const f32x16_t& x) {
+    float mt = fmaxf(fmaxf(x[0], x[1]), x[2]);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] = s[r] * c;
+    for (int r = 3; r < 15; r += 2) mt = fmaxf(mt, fmaxf(x[r], x[r + 1]));
+    mt = fmaxf(mt, x[15]);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt),
+                                                     false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+  };
+  // One phase of chunk k (rows 2k, 2k+1) of a tile held in x (in place):
+  //   0: x = S c - m (or x - m on the first tile, already scaled), overflow max
+  //   1: 2^x (underflow -> 0)
+  //   2: bf16 pack into P^T, sum of P
+  //   3: sum of bf16(P)
+  // Every phase ends by pinning what it wrote (an empty volatile asm that takes and
+  // gives the values): volatile asm keeps its place among the MFMA statements, so
+  // the optimiser can neither sink the work out of the chain nor merge phases.
+  auto sm_phase = [&](f32x16_t& x, u32x4_t(&pk)[2], int k, int ph, bool scaled) {
+    const int r = 2 * k;
+    float x0 = x[r], x1 = x[r + 1];
+    if (ph == 0) {
+      if (scaled) {
+        x0 -= m_run;
+        x1 -= m_run;
+      } else {
+        x0 = fmaf(x0, c, -m_run);
+        x1 = fmaf(x1, c, -m_run);
+      }
+      float m = fmaxf(xo, fmaxf(x0, x1));
+      asm volatile("" : "+v"(x0), "+v"(x1), "+v"(m));
+      xo = m;
+    } else if (ph == 1) {
+      x0 = __builtin_amdgcn_exp2f(x0);
+      x1 = __builtin_amdgcn_exp2f(x1);
+      asm volatile("" : "+v"(x0), "+v"(x1));
+    } else if (ph == 2) {
+      uint32_t p = pack2_q16<QT>(x0, x1);
+      float e = pe + (x0 + x1);
+      asm volatile("" : "+v"(p), "+v"(e));
+      pk[k >> 2][k & 3] = p;
+      pe = e;
+    } else {
+      float w2 = sum2_q16<QT>(pk[k >> 2][k & 3], pw);
+      asm volatile("" : "+v"(w2));
+      pw = w2;
+    }
+    x[r] = x0;
+    x[r + 1] = x1;
+  };
+  // The softmax of a tile as work items of the next tile's QK chain (steps -1 ..
+  // KSTEPS - 1).  Steady state: chunk k's phase p at step 4k + p - 1 (steps -1 ..
+  // 30).  First tile of the unit (the frame is not fixed yet): scale at steps -1
+  // and 0, the tile max at step 1, then chunk k's phase p at step 3k + p + 2
+  // (steps 2 .. 26).
+  auto sm_step = [&](f32x16_t& x, u32x4_t(&pk)[2], int ks, bool first) {
+    if (!first) {
+      const int k = (ks + 1) >> 2, ph = (ks + 1) & 3;
+      if (ks >= -1 && k < 8) sm_phase(x, pk, k, ph, false);
+    } else if (ks == -1 || ks == 0) {
+#pragma unroll
+      for (int r = 0; r < 8; r += 2) {
+        float x0 = x[8 * (ks + 1) + r] * c, x1 = x[8 * (ks + 1) + r + 1] * c;
+        asm volatile("" : "+v"(x0), "+v"(x1));
+        x[8 * (ks + 1) + r] = x0;
+        x[8 * (ks + 1) + r + 1] = x1;
+      }
+    } else if (ks == 1) {
+      float m = fmaxf(m_run, tile_max(x));
+      asm volatile("" : "+v"(m));
+      m_run = m;
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] = fmaf(s[r], c, -m_run);
+      for (int k = 0; k < 8; ++k) {
+        const int ph = ks - 2 - 3 * k;
+        if (ph >= 0 && ph < 4) sm_phase(x, pk, k, ph, true);
+      }
     }
-    if (nvalid < TILE) {  // the unit's last tile: rows past r1
+  };
+  // The unit's last tile, on its own (rows past r1 masked).
+  auto softmax_last = [&](f32x16_t& x, u32x4_t(&pk)[2], bool first, int nvalid) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] *= c;
+    if (nvalid < TILE) {
       const int lim = nvalid - 4 * g;
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (8 * (r >> 2) + (r & 3) >= lim) x[r] = -INFINITY;
     }
-    if (first) {  // O is still zero: the first tile fixes the frame
-      float mt = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    if (first) m_run = fmaxf(m_run, tile_max(x));
 #pragma unroll
-      for (int r = 4; r < 16; r += 2) mt = fmaxf(mt, fmaxf(x[r], x[r + 1]));
-      m_run = fmaxf(m_run, fmaxf(mt, __shfl_xor(mt, 32)));
+    for (int k = 0; k < 8; ++k)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] -= m_run;
-    }
-    float xm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-#pragma unroll
-    for (int r = 4; r < 16; r += 2) xm = fmaxf(xm, fmaxf(x[r], x[r + 1]));
-    xobs = fmaxf(xobs, xm);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] = __builtin_amdgcn_exp2f(x[r]);  // 2^x, underflow -> 0
-    float t8[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) t8[r] = x[2 * r] + x[2 * r + 1];
-    pe += ((t8[0] + t8[1]) + (t8[2] + t8[3])) + ((t8[4] + t8[5]) + (t8[6] + t8[7]));
-    float w2[2] = {0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pk[kk][e] = pack2_q16<QT>(x[8 * kk + 2 * e], x[8 * kk + 2 * e + 1]);
-        w2[e & 1] = sum2_q16<QT>(pk[kk][e], w2[e & 1]);
-      }
-    pw += w2[0] + w2[1];
+      for (int ph = 0; ph < 4; ++ph) sm_phase(x, pk, k, ph, true);
   };
-
 
   if (!REDO && tid == 0) sm.far = 0;
   if (ntiles > 0) {
-    // prologue: tiles 0..2 in flight, addresses of tile 3 in SGPRs
+    // Ring schedule.  Iteration i: wait for tile i+1 and barrier (tile i+1 visible;
+    // every wave is done with tile i-1), then S(i+1) = K(i+1) Q^T with the softmax
+    // of tile i and tile i+3's DMA (into tile i-1's slot) interleaved, then
+    // O += V(i)^T P(i)^T.  Tiles i, i+1 and i+3 sit in distinct slots; tiles
+    // i+2 and i+3 are in flight while i+1 is computed.  Tiles past the last one
+    // are DMA'd from the zero row, so every wait counts the same instructions.
     RowAddrs ra_next = load_addrs(0);
 #pragma unroll
     for (int k = 0; k < 8; ++k) dma_lat(0, ra_next, k);
@@ -435,39 +517,66 @@ __device__ __forceinline__ bool attend_unit(
     dma_rope(2, ra_next);
     ra_next = load_addrs(3);
 
-    // One tile: wait for it (the two younger tiles' DMAs may still be in flight),
-    // barrier (tile visible; every wave is done with tile it-1, whose slot tile
-    // it+3 reuses), S with tile it+3's DMA interleaved, softmax, PV, then the
-    // scalar loads of tile it+4's row addresses (after this tile's LDS reads, so
-    // the LDS waits above count exactly; the next barrier's lgkmcnt(0) covers them).
-    auto tile = [&](int it, bool first, bool edge) {
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * CPT, 15));
-      wait_barrier();
-      const RowAddrs ra_cur = ra_next;
-      const lds_u8* tl = tiles + (it & (NSTAGE - 1)) * TILEB;
-      const f32x16_t s = qk(tl, it + 3, ra_cur);
+    f32x16_t s_cur, s_a, s_b;
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * CPT, 15));  // tile 0 landed
+    wait_barrier();
+    qk(tiles, s_a, s_b, [](int) {});
+    // S(0) is read by VALU next: wait out the XDL-write -> VALU-read hazard
+    vgpr_mfma_drain(s_a);
+    vgpr_mfma_drain(s_b);
+    s_cur = s_a + s_b;
+
+    // One PV call site for every tile: the O accumulators are inline-assembly
+    // operands, and two call sites in the loop would be given different AGPRs,
+    // shuffled through VGPRs on every trip.
+    for (int i = 0; i < ntiles; ++i) {
       u32x4_t pk[2];
-      softmax(s, pk, first, edge ? r1 - (r0 + it * TILE) : TILE);
-      SB();
-      {
-        const int il = min(it + 4, ntiles - 1);  // dead tiles (>= ntiles) read zeros
-        ra_next = fix_tail(pv_asm(tl, pk, alist + il * TILE + 8 * wu), it + 4);
+      if (i + 1 < ntiles) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(CPT, 15));  // tile i+1 landed
+        wait_barrier();
+        const RowAddrs ra_cur = ra_next;
+        const lds_u8* tn = tiles + ((i + 1) & (NSTAGE - 1)) * TILEB;
+        if (!REDO && i == 0) {
+          qk(tn, s_a, s_b, [&](int ks) {
+            sm_step(s_cur, pk, ks, true);
+            dma_step(ks, i + 3, ra_cur);
+          });
+        } else {
+          qk(tn, s_a, s_b, [&](int ks) {
+            sm_step(s_cur, pk, ks, false);
+            dma_step(ks, i + 3, ra_cur);
+          });
+        }
+      } else {
+        softmax_last(s_cur, pk, !REDO && i == 0, r1 - (r0 + i * TILE));
       }
-    };
-    tile(0, !REDO, true);
-    for (int it = 1; it + 1 < ntiles; ++it) tile(it, false, false);
-    if (ntiles > 1) tile(ntiles - 1, false, true);
+      SB();
+      // PV of tile i, carrying the scalar load of tile i+4's row addresses (after
+      // this tile's LDS reads, so the LDS waits in it count exactly; the next
+      // barrier's lgkmcnt(0) covers the scalar load).
+      {
+        const int il = min(i + 4, ntiles - 1);  // dead tiles (>= ntiles) read zeros
+        ra_next = fix_tail(pv_asm(tiles + (i & (NSTAGE - 1)) * TILEB, pk, alist + il * TILE + 8 * wu),
+                           i + 4);
+      }
+      // S(i+1) = sa + sb becomes the tile the next trip softmaxes.  The pins order
+      // the adds after PV's 32 MFMAs, which covers the XDL-write -> VALU-read hazard
+      // of the chain's last MFMAs.
+      asm volatile("" : "+v"(s_a), "+v"(s_b));
+      s_cur = s_a + s_b;
+    }
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the dead-tile DMAs have landed
     // the last PV MFMAs (inline assembly) write the accumulators: wait out the
     // XDL-write -> VALU-read hazard before the epilogue reads them
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   }
-  pe += __shfl_xor(pe, 32);
-  pw += __shfl_xor(pw, 32);
+  float pes = pe, pws = pw, xobs = xo;
+  pes += __shfl_xor(pes, 32);
+  pws += __shfl_xor(pws, 32);
   xobs = fmaxf(xobs, __shfl_xor(xobs, 32));
   // golden.py:162-163: the sink seeds (m, l) = (sink, 1) on the token's first unit
   const float l_sink = split != 0 ? 0.f : (sink2 == m_run ? 1.f : exp2f(sink2 - m_run));
-  const float l_e = l_sink + pe, l_w = l_sink + pw;
+  const float l_e = l_sink + pes, l_w = l_sink + pws;
 
   // ---- overflow guard: a logit far above the frame redoes the whole unit ----
   if (!REDO) {
