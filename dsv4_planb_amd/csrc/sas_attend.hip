@@ -570,10 +570,16 @@ __device__ __forceinline__ bool attend_unit(
     // XDL-write -> VALU-read hazard before the epilogue reads them
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   }
+  // both half-waves of a head (lanes l and l ^ 32), summed in the same order in both
   float pes = pe, pws = pw, xobs = xo;
-  pes += __shfl_xor(pes, 32);
-  pws += __shfl_xor(pws, 32);
-  xobs = fmaxf(xobs, __shfl_xor(xobs, 32));
+  {
+    const auto a1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(pes), __float_as_uint(pes), false, false);
+    const auto a2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(pws), __float_as_uint(pws), false, false);
+    const auto a3 = __builtin_amdgcn_permlane32_swap(__float_as_uint(xobs), __float_as_uint(xobs), false, false);
+    pes = __uint_as_float(a1[0]) + __uint_as_float(a1[1]);
+    pws = __uint_as_float(a2[0]) + __uint_as_float(a2[1]);
+    xobs = fmaxf(__uint_as_float(a3[0]), __uint_as_float(a3[1]));
+  }
   // golden.py:162-163: the sink seeds (m, l) = (sink, 1) on the token's first unit
   const float l_sink = split != 0 ? 0.f : (sink2 == m_run ? 1.f : exp2f(sink2 - m_run));
   const float l_e = l_sink + pes, l_w = l_sink + pws;

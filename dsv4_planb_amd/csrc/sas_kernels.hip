@@ -225,6 +225,7 @@ __device__ __forceinline__ int paged_code(const int* __restrict__ bt_row, int ta
 // block-wide minimum) ends the list, ids outside [0, thr) are skipped, and the
 // survivors keep their slot order through a block-wide exclusive scan.
 constexpr int RS_NT = 256;
+constexpr int RS_PER = 8;  // index slots per thread and chunk
 
 __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int* __restrict__ plan,
                                                         const int* __restrict__ ori_bt,
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
                                                         const uint8_t* __restrict__ ori_kv,
                                                         const uint8_t* __restrict__ cmp_kv,
                                                         int esz) {
-  __shared__ int s_term;
+  __shared__ int s_wmin[RS_NT / 64];
   __shared__ int s_wsum[RS_NT / 64];
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
@@ -276,48 +277,76 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
   }
   const int limit = max(min(a.K, thr), 0);  // golden.py:48
   const int* ir = idx + (size_t)t * a.K;
-  const int per = (limit + RS_NT - 1) / RS_NT;
-  const int s0 = min(tid * per, limit), s1 = min(s0 + per, limit);
-  if (tid == 0) s_term = limit;
-  __syncthreads();
-  // golden.py:52-53: the first -1 terminates the list
-  for (int i = s0; i < s1; ++i)
-    if (ir[i] == -1) {
-      atomicMin(&s_term, i);
-      break;
-    }
-  __syncthreads();
-  const int term = s_term;
-  int cnt = 0;
-  for (int i = s0; i < min(s1, term); ++i) {
-    const int id = ir[i];
-    cnt += (id >= 0 && id < thr);  // golden.py:58-59: ids at or beyond thr are skipped
-  }
-  // block-wide exclusive scan of cnt
-  int incl = cnt;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int v = __shfl_up(incl, off);
-    if (lane >= off) incl += v;
-  }
-  if (lane == 63) s_wsum[w] = incl;
-  __syncthreads();
-  int base = incl - cnt;
-  for (int j = 0; j < w; ++j) base += s_wsum[j];
   const int* cbt = cmp_bt + (size_t)b * a.cmp_table_len;
-  for (int i = s0; i < min(s1, term); ++i) {
-    const int id = ir[i];
-    if (id >= 0 && id < thr) {
-      const int code = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, id);
-      out[base] = code;
-      aout[base++] = code_addr(code, cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
+  // Chunks of RS_NT * RS_PER slots; thread tid owns slots [RS_PER tid, RS_PER (tid + 1))
+  // of a chunk and loads them all before using any (one memory round trip), then
+  // the terminator, the survivors and their slot-order positions come from
+  // block-wide reductions over registers.
+  const bool vec = (a.K & 3) == 0;  // index rows are 16-B aligned
+  int emitted = 0;                  // compressed rows written so far (block-uniform)
+  for (int c0 = 0; c0 < limit; c0 += RS_NT * RS_PER) {
+    const int s0 = c0 + tid * RS_PER;
+    int v[RS_PER];
+    if (vec && s0 + RS_PER <= limit) {
+#pragma unroll
+      for (int k = 0; k < RS_PER; k += 4) {
+        const int4 x = *reinterpret_cast<const int4*>(ir + s0 + k);
+        v[k] = x.x;
+        v[k + 1] = x.y;
+        v[k + 2] = x.z;
+        v[k + 3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < RS_PER; ++k) v[k] = s0 + k < limit ? ir[s0 + k] : -2;
     }
+    // golden.py:52-53: the first -1 terminates the list
+    int first = limit;
+#pragma unroll
+    for (int k = RS_PER - 1; k >= 0; --k)
+      if (v[k] == -1) first = s0 + k;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) first = min(first, __shfl_xor(first, off));
+    if (lane == 0) s_wmin[w] = first;
+    __syncthreads();
+    int term = s_wmin[0];
+#pragma unroll
+    for (int j = 1; j < RS_NT / 64; ++j) term = min(term, s_wmin[j]);
+    // golden.py:58-59: ids at or beyond thr are skipped (other negatives too)
+    int cnt = 0;
+    unsigned keep = 0;
+#pragma unroll
+    for (int k = 0; k < RS_PER; ++k)
+      if (s0 + k < term && v[k] >= 0 && v[k] < thr) {
+        keep |= 1u << k;
+        ++cnt;
+      }
+    // block-wide exclusive scan of cnt: survivors keep their slot order
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int x = __shfl_up(incl, off);
+      if (lane >= off) incl += x;
+    }
+    if (lane == 63) s_wsum[w] = incl;
+    __syncthreads();
+    int pos = emitted + incl - cnt, total = 0;
+#pragma unroll
+    for (int j = 0; j < RS_NT / 64; ++j) {
+      if (j < w) pos += s_wsum[j];
+      total += s_wsum[j];
+    }
+#pragma unroll
+    for (int k = 0; k < RS_PER; ++k)
+      if ((keep >> k) & 1u) {
+        const int code = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, v[k]);
+        out[pos] = code;
+        aout[pos++] = code_addr(code, cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
+      }
+    emitted += total;
+    if (term < limit) break;  // the list ended in this chunk
   }
-  if (tid == RS_NT - 1) {
-    int total = 0;
-    for (int j = 0; j < RS_NT / 64; ++j) total += s_wsum[j];
-    ncmp_out[t] = total;
-  }
+  if (tid == 0) ncmp_out[t] = emitted;
 }
 
 // ===========================================================================

@@ -134,19 +134,36 @@ def test_large_logits_d576_reference_draws():
     _check("large-logits", c, rule="reference")
 
 
-def test_resolution_bit_exact():
+def _resolution_case(kind):
+    if kind == "k300":
+        c = make_case(B=5, H=16, seq_kv=[130, 4000, 64, 9000, 2], q_per_seq=[1, 2, 4, 3, 2],
+                      scenario=3, K=300, seed=11)
+        c.idx[2, 1] = -1
+        c.idx[4, 0] = 99_999
+        c.ori_block_table[1, 3] = -1  # an unused page inside the window reads as zeros
+        return c
+    # K = 4100: more slots than one pass of the resolver takes (2048), vector loads,
+    # a partial last pass; a terminator and skipped ids past the first pass
+    c = make_case(B=3, H=16, seq_kv=[20000, 30000, 17000], q_per_seq=[1, 2, 1], scenario=3,
+                  K=4100, seed=13)
+    c.idx[0, 3000] = -1
+    c.idx[1, 2100] = 1_000_000
+    c.idx[1, 4099] = 1_000_000
+    c.idx[2, 2047] = -1           # the last slot of the first pass ends the list
+    c.idx[3, 2048] = -1           # the first slot of the second pass ends the list
+    return c
+
+
+@pytest.mark.parametrize("kind", ["k300", "k4100"])
+def test_resolution_bit_exact(kind):
     """Window and compressed row codes (paged pool rows, -1 = zero row) and the
     compressed counts equal the oracle's resolution exactly."""
     from oracle import golden_c
     from dsv4_planb_amd import _lib
     from dsv4_planb_amd.api import build_launch
 
-    c = make_case(B=5, H=16, seq_kv=[130, 4000, 64, 9000, 2], q_per_seq=[1, 2, 4, 3, 2],
-                  scenario=3, K=300, seed=11)
-    c.idx[2, 1] = -1
-    c.idx[4, 0] = 99_999
-    c.ori_block_table[1, 3] = -1  # an unused page inside the window reads as zeros
-    _banner("resolve", c)
+    c = _resolution_case(kind)
+    _banner("resolve-" + kind, c)
     d = to_device(c)
     launch, out, lse = build_launch(
         q_flat=d["q"], ori_kv=d["ori_kv"], ori_block_table=d["ori_block_table"],
