@@ -209,6 +209,66 @@ def _traffic_from_profile(workload):
 
 
 # ---------------------------------------------------------------------------
+# On-box peaks: what this GPU sustains for the two bounds the roofline uses
+# ---------------------------------------------------------------------------
+def measure_peaks(dev, secs=2.0):
+    """Sustained bf16 MFMA rate (register-only, random operands that change every
+    MFMA, one wave per SIMD) and HBM read bandwidth (16-B streaming loads over
+    4 GiB), each after `secs` of back-to-back launches so the clock has settled
+    under the power limit.  Kernels: dsv4_planb_amd/csrc/sas_probe.hip."""
+    import ctypes
+
+    from dsv4_planb_amd.build import PROBE_LIB
+
+    if not os.path.exists(PROBE_LIB):
+        raise RuntimeError(f"{PROBE_LIB} missing: run __graft_entry__.build()")
+    lib = ctypes.CDLL(PROBE_LIB)
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def sustained(fn, n_timed):
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < secs:
+            fn()
+            torch.cuda.synchronize()
+        return _events_time(fn, n_timed, stream)
+
+    blocks, iters = 256, 16000  # 1024 waves: one per SIMD
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    ticks = torch.zeros(blocks * 4, dtype=torch.int64, device=dev)
+
+    def mfma():
+        rc = lib.sas_probe_mfma(ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ticks.data_ptr()),
+                                iters, blocks, sp)
+        if rc:
+            raise RuntimeError(f"sas_probe_mfma: {rc}")
+
+    us = sustained(mfma, 10)
+    mfma_tflops = blocks * 4 * iters * 8 * 32768 / (us * 1e-6) / 1e12
+    clock_ghz = float(ticks.double().mean().item()) / (us * 1e-6) / 1e9
+    del out, ticks
+    nbytes = 4 << 30
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    rblocks = 2048
+    rout = torch.empty(rblocks * 256, dtype=torch.int32, device=dev)
+
+    def read():
+        rc = lib.sas_probe_read(ctypes.c_void_p(src.data_ptr()), ctypes.c_size_t(nbytes),
+                                ctypes.c_void_p(rout.data_ptr()), rblocks, sp)
+        if rc:
+            raise RuntimeError(f"sas_probe_read: {rc}")
+
+    us_r = sustained(read, 10)
+    del src, rout
+    torch.cuda.empty_cache()
+    return {"mfma_bf16_tflops": round(mfma_tflops, 1), "mfma_clock_ghz": round(clock_ghz, 3),
+            "hbm_read_gbs": round(nbytes / (us_r * 1e-6) / 1e9, 1),
+            "method": "sas_probe.hip: 32x32x16 bf16 MFMA on random operands, 1 wave/SIMD, "
+                      "register-only; 16-B streaming reads of 4 GiB; each sustained for "
+                      f"{secs:.0f} s before 10 timed launches"}
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline: the C oracle on a bounded sample of the same workload
 # ---------------------------------------------------------------------------
 def cpu_baseline(name, n_seq, seed=0):
@@ -322,6 +382,8 @@ def main():
     ap.add_argument("--cpu-seqs", type=int, default=0,
                     help="cap on sampled sequences for the CPU baseline (0 = size for ~10 s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-peaks", action="store_true",
+                    help="skip the on-box MFMA / HBM peak probes")
     ap.add_argument("--mode", default="bench", choices=["bench", "attend", "copy"],
                     help="bench: the JSON line; attend: only the attention stage of --workload, "
                          "--steps launches (for counter runs); copy: a 1 GiB device copy, "
@@ -368,12 +430,24 @@ def main():
 
     main_r = results[args.workload]
     bound = "mfma" if args.workload == "prefill8k" else "hbm"
+    peaks = None
+    if not args.no_peaks:
+        _log("on-box peaks")
+        peaks = measure_peaks(dev)
     if bound == "hbm":
         ach, peak, unit = main_r["attend_gbs"], HBM_PEAK_GBS, "GB/s"
+        measured = peaks["hbm_read_gbs"] if peaks else None
     else:
         ach, peak, unit = main_r["attend_tflops"], MFMA_BF16_PEAK_TFLOPS, "TFLOP/s"
+        measured = peaks["mfma_bf16_tflops"] if peaks else None
+    if peaks:
+        for r in results.values():
+            r["frac_hbm_measured"] = round(r["attend_gbs"] / peaks["hbm_read_gbs"], 4)
+            r["frac_mfma_measured"] = round(r["attend_tflops"] / peaks["mfma_bf16_tflops"], 4)
     roofline = {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
                 "frac": round(ach / peak, 4), "traffic": _traffic_from_profile(args.workload),
+                "measured_peak": measured,
+                "frac_of_measured": round(ach / measured, 4) if measured else None,
                 "kernel": "sas::attend_kernel<576, bf16>", "kernel_us": round(main_r["attend_us"], 2),
                 "algorithmic_bytes": main_r["alg_bytes"], "algorithmic_flops": main_r["alg_flops"]}
     cpu = None
@@ -410,6 +484,7 @@ def main():
         "data": "synthetic (seeded N(0,1) bf16 q/KV, random page permutation, random top-k)",
         "config": {"workload": desc[args.workload], "name": args.workload},
         "roofline": roofline,
+        "measured_peaks": peaks,
         "cpu_baseline": cpu,
         "workloads": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                       for k, v in results.items()},

@@ -1,8 +1,9 @@
 """Build ``libsas_hip.so`` (gfx950) in-tree with hipcc.
 
 The library holds the HIP kernels, the C ABI of ``include/sas.h`` and the host
-restatement of the reference metadata scheduler.  The output lands next to this
-file so it travels with the source tree.
+restatement of the reference metadata scheduler.  ``libsas_probe.so`` holds the
+on-box peak probes the benchmark rates the kernels against.  The outputs land
+next to this file so they travel with the source tree.
 """
 
 from __future__ import annotations
@@ -15,6 +16,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libsas_hip.so")
+PROBE_LIB = os.path.join(HERE, "libsas_probe.so")  # on-box peak probes (benchmark only)
 OBJ_DIR = os.path.join(HERE, "_build")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -49,6 +51,10 @@ def build(verbose: bool = False) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", o_hip, o_meta, "-o", tmp], verbose)
     os.replace(tmp, LIB)
+    tmp = PROBE_LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", *COMMON, *DEVICE_FLAGS, "-shared",
+          os.path.join(CSRC, "sas_probe.hip"), "-o", tmp], verbose)
+    os.replace(tmp, PROBE_LIB)
     return LIB
 
 

@@ -207,6 +207,37 @@ __device__ __forceinline__ bool attend_unit(
   const int h = w * 32 + li;
   const bool hvalid = h < H;
   const int hc = min(h, H - 1);
+  // golden.py:162-163: the unit holding the token's first rows carries the sink
+  const float sink2 = split == 0 ? sinks[hc] * LOG2E : -INFINITY;
+
+  // A unit without rows (a redo always has some): O = 0 and the normalisers are
+  // the sink's alone.  Returning here also keeps the accumulators below on a
+  // single path, so the epilogue does not have to merge them with zeros.
+  if (ntiles == 0) {
+    if (REDO || !hvalid) return false;
+    const float l_sink = split == 0 ? 1.f : 0.f;
+    if (splits == 1) {
+      uint16_t* orow = out + ((size_t)t * H + h) * DV + 16 * g;
+#pragma unroll
+      for (int mb = 0; mb < 16; ++mb)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+          *reinterpret_cast<u32x4_t*>(orow + 32 * mb + 8 * hf) = u32x4_t{0, 0, 0, 0};
+      if (lse && g == 0) lse[(size_t)t * H + h] = (sink2 + __log2f(l_sink)) * 0.6931471805599453f;
+    } else {
+      const int slot = wsbase + split;
+      float* orow = ws_o + ((size_t)slot * H + h) * DV + 16 * g;
+#pragma unroll
+      for (int mb = 0; mb < 16; ++mb)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd)
+          *reinterpret_cast<float4*>(orow + 32 * mb + 4 * qd) = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (g == 0)
+        reinterpret_cast<float4*>(ws_ml)[(size_t)slot * H + h] = make_float4(sink2, l_sink, l_sink, 0.f);
+    }
+    return false;
+  }
+
   u32x4_t qf[KSTEPS];
   {
     const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(q + ((size_t)t * H + hc) * DQK);
@@ -216,8 +247,6 @@ __device__ __forceinline__ bool attend_unit(
   f32x16_t acc[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = f32x16_t{};
-  // golden.py:162-163: the unit holding the token's first rows carries the sink
-  const float sink2 = split == 0 ? sinks[hc] * LOG2E : -INFINITY;
   float m_run = REDO ? m_obs : sink2;  // redo: the frame is the maximum pass 1 observed
 
   // ---- gather: tile i goes to ring slot i & 3 ----
@@ -496,7 +525,7 @@ __device__ __forceinline__ bool attend_unit(
   };
 
   if (!REDO && tid == 0) sm.far = 0;
-  if (ntiles > 0) {
+  {  // ntiles >= 1
     // Ring schedule.  Iteration i: wait for tile i+1 and barrier (tile i+1 visible;
     // every wave is done with tile i-1), then S(i+1) = K(i+1) Q^T with the softmax
     // of tile i and tile i+3's DMA (into tile i-1's slot) interleaved, then
@@ -599,15 +628,19 @@ __device__ __forceinline__ bool attend_unit(
   if (splits == 1) {
     const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
     uint16_t* orow = out + ((size_t)t * H + h) * DV + 16 * g;
+    // One 16-register block at a time into VGPRs (the pin keeps the copies in
+    // step with the stores: copied all at once, the 256 accumulators overflow
+    // the VGPRs and spill).
 #pragma unroll
     for (int mb = 0; mb < 16; ++mb) {
+      f32x16_t v = acc[mb];
+      asm volatile("" : "+v"(v));
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         u32x4_t o;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          o[e] = to_q16<QT>(acc[mb][8 * hf + 2 * e] * inv) |
-                 (to_q16<QT>(acc[mb][8 * hf + 2 * e + 1] * inv) << 16);
+          o[e] = pack2_q16<QT>(v[8 * hf + 2 * e] * inv, v[8 * hf + 2 * e + 1] * inv);
         *reinterpret_cast<u32x4_t*>(orow + 32 * mb + 8 * hf) = o;
       }
     }
