@@ -237,15 +237,20 @@ def measure_peaks(dev, secs=2.0):
     out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
     ticks = torch.zeros(blocks * 4, dtype=torch.int64, device=dev)
 
-    def mfma():
+    def mfma(dep=0):
         rc = lib.sas_probe_mfma(ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ticks.data_ptr()),
-                                iters, blocks, sp)
+                                iters, blocks, dep, sp)
         if rc:
             raise RuntimeError(f"sas_probe_mfma: {rc}")
 
     us = sustained(mfma, 10)
-    mfma_tflops = blocks * 4 * iters * 8 * 32768 / (us * 1e-6) / 1e12
+    n_mfma = iters * 8  # per wave
+    mfma_tflops = blocks * 4 * n_mfma * 32768 / (us * 1e-6) / 1e12
     clock_ghz = float(ticks.double().mean().item()) / (us * 1e-6) / 1e9
+    indep_cycles = float(ticks.double().mean().item()) / n_mfma
+    mfma(1)  # one dependent chain per wave: cycles per MFMA when each waits for the last
+    torch.cuda.synchronize()
+    dep_cycles = float(ticks.double().mean().item()) / n_mfma
     del out, ticks
     nbytes = 4 << 30
     src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -262,6 +267,7 @@ def measure_peaks(dev, secs=2.0):
     del src, rout
     torch.cuda.empty_cache()
     return {"mfma_bf16_tflops": round(mfma_tflops, 1), "mfma_clock_ghz": round(clock_ghz, 3),
+            "mfma_cycles_independent": round(indep_cycles, 2), "mfma_cycles_dependent": round(dep_cycles, 2),
             "hbm_read_gbs": round(nbytes / (us_r * 1e-6) / 1e9, 1),
             "method": "sas_probe.hip: 32x32x16 bf16 MFMA on random operands, 1 wave/SIMD, "
                       "register-only; 16-B streaming reads of 4 GiB; each sustained for "
@@ -365,6 +371,92 @@ def profile_attend(name, steps, dev, core_num=256):
                       "alg_bytes": wl["alg_bytes"], "alg_flops": wl["alg_flops"]}))
 
 
+def _smi_sample():
+    """Socket power (W) and GFX clocks (MHz) from one `amd-smi metric -p -c` call."""
+    import subprocess
+
+    try:
+        txt = subprocess.run(["amd-smi", "metric", "-p", "-c"], capture_output=True, text=True,
+                             timeout=30).stdout
+    except Exception as e:  # noqa: BLE001
+        return {"error": str(e)}
+    power, clocks, in_gfx = None, [], False
+    for line in txt.splitlines():
+        s = line.strip()
+        if s.startswith("SOCKET_POWER:"):
+            power = s.split(":", 1)[1].strip()
+        elif s.startswith("GFX_"):
+            in_gfx = True
+        elif s.endswith(":") and not s.startswith("GFX_"):
+            in_gfx = False
+        elif in_gfx and s.startswith("CLK:"):
+            clocks.append(s.split(":", 1)[1].strip())
+            in_gfx = False
+    return {"socket_power": power, "gfx_clk": clocks}
+
+
+def power_mode(name, secs, dev):
+    """Run one stage back to back for `secs` s and sample power / clocks halfway:
+    the attention stage of a workload, or a peak probe ('mfma_probe', 'read_probe')."""
+    import ctypes
+
+    stream = torch.cuda.current_stream(dev)
+    if name in ("mfma_probe", "read_probe"):
+        from dsv4_planb_amd.build import PROBE_LIB
+
+        lib = ctypes.CDLL(PROBE_LIB)
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        if name == "mfma_probe":
+            out = torch.empty(256 * 256, dtype=torch.float32, device=dev)
+            ticks = torch.zeros(256 * 4, dtype=torch.int64, device=dev)
+            fn = lambda: lib.sas_probe_mfma(ctypes.c_void_p(out.data_ptr()),  # noqa: E731
+                                            ctypes.c_void_p(ticks.data_ptr()), 16000, 256, 0, sp)
+        else:
+            src = torch.empty(4 << 30, dtype=torch.uint8, device=dev)
+            out = torch.empty(2048 * 256, dtype=torch.int32, device=dev)
+            fn = lambda: lib.sas_probe_read(ctypes.c_void_p(src.data_ptr()),  # noqa: E731
+                                            ctypes.c_size_t(4 << 30), ctypes.c_void_p(out.data_ptr()),
+                                            2048, sp)
+    else:
+        from dsv4_planb_amd import metadata as M
+        from dsv4_planb_amd.api import build_launch
+
+        wl = make_workload(name, seed=0, dev=dev)
+        cu = wl["cu"]
+        plan = M.sparse_attn_sharedkv_metadata(
+            num_heads_q=wl["H"], num_heads_kv=1, head_dim=D_QK, cu_seqlens_q=cu,
+            seqused_kv=wl["seqused"], batch_size=wl["B"], max_seqlen_q=wl["q_per"],
+            max_seqlen_kv=max(wl["kv"]), cmp_topk=wl["K"], cmp_ratio=RATIO, layout_q="TND",
+            has_cmp_kv=True, aic_core_num=256)
+        launch, _, _ = build_launch(
+            q_flat=wl["q"], ori_kv=wl["ori_kv"], ori_block_table=wl["ori_bt"], cmp_kv=wl["cmp_kv"],
+            cmp_block_table=wl["cmp_bt"], cmp_indices=wl["idx"], q_prefix=cu[:-1],
+            act_q_lens=cu[1:] - cu[:-1], seqused_kv=wl["seqused"], sinks=wl["sinks"],
+            metadata=plan, scenario=3, topk=wl["K"], cmp_ratio=RATIO, ori_win_left=WIN - 1,
+            softmax_scale=1.0 / math.sqrt(D_QK), core_num=256)
+        launch.run("resolve")
+        fn = lambda: launch.run("attend")  # noqa: E731
+    idle = _smi_sample()
+    fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n, sample = 0, None
+    while time.perf_counter() - t0 < secs:
+        fn()
+        n += 1
+        if sample is None and time.perf_counter() - t0 > secs / 2:
+            for _ in range(5):  # keep the queue full while sampling
+                fn()
+            n += 5
+            sample = _smi_sample()
+        if n % 20 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    print(json.dumps({"mode": "power", "stage": name, "launches": n, "us_per_launch": round(dt / n * 1e6, 1),
+                      "under_load": sample, "before": idle}))
+
+
 def main_r_batch(name):
     return dict(decode128k=128, decode32=32, prefill8k=1)[name]
 
@@ -384,10 +476,15 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-peaks", action="store_true",
                     help="skip the on-box MFMA / HBM peak probes")
-    ap.add_argument("--mode", default="bench", choices=["bench", "attend", "copy"],
+    ap.add_argument("--mode", default="bench", choices=["bench", "attend", "copy", "power"],
                     help="bench: the JSON line; attend: only the attention stage of --workload, "
                          "--steps launches (for counter runs); copy: a 1 GiB device copy, "
-                         "--steps times (calibrates the HBM byte counters)")
+                         "--steps times (calibrates the HBM byte counters); power: --stage back "
+                         "to back for --secs with a power / clock sample")
+    ap.add_argument("--stage", default="decode128k",
+                    choices=["decode128k", "prefill8k", "decode32", "mfma_probe", "read_probe"],
+                    help="what --mode power runs")
+    ap.add_argument("--secs", type=float, default=10.0, help="--mode power duration")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -409,6 +506,9 @@ def main():
         return
     if args.mode == "attend":
         profile_attend(args.workload, args.steps, dev)
+        return
+    if args.mode == "power":
+        power_mode(args.stage, args.secs, dev)
         return
     results = {}
     for name in [args.workload] + [w for w in args.extra.split(",") if w and w != args.workload]:

@@ -314,10 +314,7 @@ __device__ __forceinline__ bool attend_unit(
     return ks < 32 ? lds_read_b128(tl + kofs[ks & 1] + 64 * (ks >> 1))
                    : lds_read_b128(tl + (kr ^ (32u * (uint32_t)(ks - 32))));
   };
-  // Even and odd k-steps accumulate into sa and sb: an MFMA that accumulates into
-  // the previous one's result waits for it (44 instead of 32 cycles), so the chain
-  // alternates between two accumulators; S = sa + sb.
-  auto qk = [&](const lds_u8* tl, f32x16_t& sa, f32x16_t& sb, auto&& work) {
+  auto qk = [&](const lds_u8* tl, f32x16_t& s, auto&& work) {
     // the rope offset, formed per chain rather than kept across the loop
     uint32_t kr = kofs_r;
     asm volatile("" : "+v"(kr));
@@ -328,17 +325,13 @@ __device__ __forceinline__ bool attend_unit(
     SB();
     work(-1);
     SB();
-    vmfma_first<QT>(sa, kb[0], qf[0]);
+    vmfma_first<QT>(s, kb[0], qf[0]);
     work(0);
     SB();
-    kb[0] = kread(tl, 3, kr);
-    vmfma_first<QT>(sb, kb[1], qf[1]);
-    work(1);
-    SB();
 #pragma unroll
-    for (int ks = 2; ks < KSTEPS; ++ks) {
+    for (int ks = 1; ks < KSTEPS; ++ks) {
       if (ks + 2 < KSTEPS) kb[(ks + 2) % 3] = kread(tl, ks + 2, kr);
-      vmfma_acc<QT>((ks & 1) ? sb : sa, kb[ks % 3], qf[ks]);
+      vmfma_acc<QT>(s, kb[ks % 3], qf[ks]);
       work(ks);
       SB();
     }
@@ -356,9 +349,7 @@ __device__ __forceinline__ bool attend_unit(
   // own LDS waits count only the V^T reads (a scalar load in flight can only make
   // them stricter), so the loaded SGPRs are valid when the block ends.
   // V^T operand ring: three 4-VGPR buffers v[244:255] (clobbered), reads 3 MFMAs ahead.
-  // The MFMAs run accumulator-outer (all 16 d-blocks of key half 0, then of half 1):
-  // an MFMA that accumulates into the previous one's result waits for it (44
-  // instead of 32 cycles on gfx950), so no two consecutive MFMAs share one.
+  // The MFMAs run accumulator-outer: all 16 d-blocks of key half 0, then of half 1.
   auto pv_asm = [&](const lds_u8* tl, const u32x4_t(&pk)[2], const uint64_t* aptr) -> RowAddrs {
     const uint32_t a0 = (uint32_t)(uintptr_t)tl + vofs[0];
     const uint32_t a1 = (uint32_t)(uintptr_t)tl + vofs[1];
@@ -546,14 +537,12 @@ __device__ __forceinline__ bool attend_unit(
     dma_rope(2, ra_next);
     ra_next = load_addrs(3);
 
-    f32x16_t s_cur, s_a, s_b;
+    f32x16_t s_cur, s_next;
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * CPT, 15));  // tile 0 landed
     wait_barrier();
-    qk(tiles, s_a, s_b, [](int) {});
+    qk(tiles, s_cur, [](int) {});
     // S(0) is read by VALU next: wait out the XDL-write -> VALU-read hazard
-    vgpr_mfma_drain(s_a);
-    vgpr_mfma_drain(s_b);
-    s_cur = s_a + s_b;
+    vgpr_mfma_drain(s_cur);
 
     // One PV call site for every tile: the O accumulators are inline-assembly
     // operands, and two call sites in the loop would be given different AGPRs,
@@ -566,12 +555,12 @@ __device__ __forceinline__ bool attend_unit(
         const RowAddrs ra_cur = ra_next;
         const lds_u8* tn = tiles + ((i + 1) & (NSTAGE - 1)) * TILEB;
         if (!REDO && i == 0) {
-          qk(tn, s_a, s_b, [&](int ks) {
+          qk(tn, s_next, [&](int ks) {
             sm_step(s_cur, pk, ks, true);
             dma_step(ks, i + 3, ra_cur);
           });
         } else {
-          qk(tn, s_a, s_b, [&](int ks) {
+          qk(tn, s_next, [&](int ks) {
             sm_step(s_cur, pk, ks, false);
             dma_step(ks, i + 3, ra_cur);
           });
@@ -588,11 +577,11 @@ __device__ __forceinline__ bool attend_unit(
         ra_next = fix_tail(pv_asm(tiles + (i & (NSTAGE - 1)) * TILEB, pk, alist + il * TILE + 8 * wu),
                            i + 4);
       }
-      // S(i+1) = sa + sb becomes the tile the next trip softmaxes.  The pins order
-      // the adds after PV's 32 MFMAs, which covers the XDL-write -> VALU-read hazard
-      // of the chain's last MFMAs.
-      asm volatile("" : "+v"(s_a), "+v"(s_b));
-      s_cur = s_a + s_b;
+      // S(i+1) becomes the tile the next trip softmaxes.  The pin orders the copy
+      // after PV's 32 MFMAs, which covers the XDL-write -> VALU-read hazard of the
+      // chain's last MFMA.
+      asm volatile("" : "+v"(s_next));
+      s_cur = s_next;
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // the dead-tile DMAs have landed
     // the last PV MFMAs (inline assembly) write the accumulators: wait out the

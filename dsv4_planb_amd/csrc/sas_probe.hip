@@ -2,10 +2,11 @@
 // (libsas_probe.so; measurement only, not part of the operator's C ABI).
 //
 //   sas_probe_mfma   register-only v_mfma_f32_32x32x16_bf16 throughput: each wave
-//                    keeps 8 independent accumulators and cycles its A and B operands
-//                    through 8 fragments each of pseudo-random bf16 values, so the
-//                    operands change on every MFMA (operand toggling sets the power the
-//                    matrix cores draw, and with it the clock they sustain).
+//                    keeps 8 independent accumulators (or, `dependent`, one chain)
+//                    and cycles its A and B operands through 8 fragments each of
+//                    pseudo-random bf16 values, so the operands change on every MFMA
+//                    (operand toggling sets the power the matrix cores draw, and with
+//                    it the clock they sustain).
 //   sas_probe_read   streaming 16-byte loads over a buffer (HBM read bandwidth).
 //
 // Both write one value per thread (out[blockIdx.x * 256 + threadIdx.x]) so that the
@@ -37,6 +38,9 @@ __device__ __forceinline__ uint32_t rnd_bf16x2(uint32_t h) {
   return (lo & 0xffffu) | (hi << 16);
 }
 
+// NACC independent accumulators per wave (8: throughput; 1: one dependent chain,
+// each MFMA accumulating into the previous one's result).
+template <int NACC>
 __global__ __launch_bounds__(256) void probe_mfma_kernel(float* __restrict__ out,
                                                          uint64_t* __restrict__ ticks, int iters) {
   u32x4_t A[8], B[8];
@@ -46,21 +50,21 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(float* __restrict__ out
       A[i][e] = rnd_bf16x2(mix32(seed + 97u * i + e));
       B[i][e] = rnd_bf16x2(mix32(seed * 31u + 89u * i + e + 7u));
     }
-  f32x16_t acc[8];
-  for (int k = 0; k < 8; ++k) acc[k] = f32x16_t{};
+  f32x16_t acc[NACC];
+  for (int k = 0; k < NACC; ++k) acc[k] = f32x16_t{};
   const uint64_t t0 = __builtin_amdgcn_s_memtime();
   for (int it = 0; it < iters; it += 8) {
 #pragma unroll
     for (int u = 0; u < 8; ++u)
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        acc[k % NACC] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             __builtin_bit_cast(bf16x8_t, A[(k + u) & 7]), __builtin_bit_cast(bf16x8_t, B[(3 * k + u) & 7]),
-            acc[k], 0, 0, 0);
+            acc[k % NACC], 0, 0, 0);
   }
   const uint64_t t1 = __builtin_amdgcn_s_memtime();
   float s = 0.f;
-  for (int k = 0; k < 8; ++k)
+  for (int k = 0; k < NACC; ++k)
     for (int r = 0; r < 16; ++r) s += acc[k][r];
   const size_t gid = (size_t)blockIdx.x * 256 + threadIdx.x;
   out[gid] = s;
@@ -84,11 +88,16 @@ __global__ __launch_bounds__(256) void probe_read_kernel(const u32x4_t* __restri
 
 extern "C" {
 
-// iters: MFMA rounds per wave (a multiple of 8); ticks: blocks * 4 per-wave s_memtime spans.
-int sas_probe_mfma(float* out, uint64_t* ticks, int iters, int blocks, void* stream) {
+// iters: rounds of 8 MFMAs per wave (a multiple of 8); ticks: blocks * 4 per-wave
+// s_memtime spans (shader clock cycles).  dependent != 0: one accumulator per wave.
+int sas_probe_mfma(float* out, uint64_t* ticks, int iters, int blocks, int dependent, void* stream) {
   if (!out || !ticks || iters <= 0 || (iters & 7) || blocks <= 0) return -1;
-  hipLaunchKernelGGL(probe_mfma_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out, ticks,
-                     iters);
+  if (dependent)
+    hipLaunchKernelGGL(probe_mfma_kernel<1>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out,
+                       ticks, iters);
+  else
+    hipLaunchKernelGGL(probe_mfma_kernel<8>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, out,
+                       ticks, iters);
   return hipGetLastError() == hipSuccess ? 0 : -9;
 }
 
