@@ -55,7 +55,10 @@ def _random_subsets(n_tok, thr, K, space, gen, dev):
                        torch.full_like(order, -1))
 
 
-def make_workload(name: str, seed: int = 0, dev="cuda"):
+def make_workload(name: str, seed: int = 0, dev="cuda", compact: bool = False):
+    """Synthetic inputs of one workload.  compact: every sequence's block tables
+    point at the first sequence's pages (a KV footprint that fits the 256 MB MALL;
+    for locality experiments only, never the benchmark figure)."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     if name == "decode128k":
@@ -85,6 +88,9 @@ def make_workload(name: str, seed: int = 0, dev="cuda"):
         cbt[b, :cpages[b]] = cperm[c:c + cpages[b]]
         o += pages[b]
         c += cpages[b]
+    if compact:
+        obt[:, :] = obt[0:1, :].clone()
+        cbt[:, :] = cbt[0:1, :].clone()
     q = torch.randn((T, H, D_QK), dtype=torch.bfloat16, device=dev, generator=gen)
     sinks = (torch.rand(H, device=dev, generator=gen) * 2 - 1).float()
     cu = torch.arange(0, T + 1, q_per, dtype=torch.int32, device=dev)
@@ -395,7 +401,7 @@ def _smi_sample():
     return {"socket_power": power, "gfx_clk": clocks}
 
 
-def power_mode(name, secs, dev):
+def power_mode(name, secs, dev, compact=False):
     """Run one stage back to back for `secs` s and sample power / clocks halfway:
     the attention stage of a workload, or a peak probe ('mfma_probe', 'read_probe')."""
     import ctypes
@@ -421,7 +427,7 @@ def power_mode(name, secs, dev):
         from dsv4_planb_amd import metadata as M
         from dsv4_planb_amd.api import build_launch
 
-        wl = make_workload(name, seed=0, dev=dev)
+        wl = make_workload(name, seed=0, dev=dev, compact=compact)
         cu = wl["cu"]
         plan = M.sparse_attn_sharedkv_metadata(
             num_heads_q=wl["H"], num_heads_kv=1, head_dim=D_QK, cu_seqlens_q=cu,
@@ -453,7 +459,8 @@ def power_mode(name, secs, dev):
             torch.cuda.synchronize()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    print(json.dumps({"mode": "power", "stage": name, "launches": n, "us_per_launch": round(dt / n * 1e6, 1),
+    print(json.dumps({"mode": "power", "stage": name, "compact": compact, "launches": n,
+                      "us_per_launch": round(dt / n * 1e6, 1),
                       "under_load": sample, "before": idle}))
 
 
@@ -485,6 +492,8 @@ def main():
                     choices=["decode128k", "prefill8k", "decode32", "mfma_probe", "read_probe"],
                     help="what --mode power runs")
     ap.add_argument("--secs", type=float, default=10.0, help="--mode power duration")
+    ap.add_argument("--compact", action="store_true",
+                    help="--mode power: all sequences read the first sequence's KV pages")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -508,7 +517,7 @@ def main():
         profile_attend(args.workload, args.steps, dev)
         return
     if args.mode == "power":
-        power_mode(args.stage, args.secs, dev)
+        power_mode(args.stage, args.secs, dev, compact=args.compact)
         return
     results = {}
     for name in [args.workload] + [w for w in args.extra.split(",") if w and w != args.workload]:

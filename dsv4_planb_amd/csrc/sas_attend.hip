@@ -5,18 +5,22 @@
 // its compressed rows).  Wave w owns query heads [32 w, 32 w + 32); Q stays in
 // VGPRs (36 x 16-B fragments at d_qk = 576) and the fp32 O^T accumulator of
 // 512 x 32 fills the AGPRs.  KV rows are gathered 32 at a time (one tile) by
-// buffer loads that write LDS directly, into a 4-slot ring, three tiles ahead
-// of the one being consumed.
+// buffer loads that write LDS directly, into a 4-slot ring.
 //
-// Per tile, per wave (32 keys x 32 heads):
-//   S^T = K Q^T      36 MFMA 32x32x16 into a VGPR accumulator, A = K rows from LDS
-//                    (ds_read_b128, three ahead), B = Q; tile it+3's DMA is
-//                    spread over the chain
-//   softmax          P = 2^(x - m) in a per-unit frame m, bf16(P)
-//   O^T += V^T P^T   32 MFMA into the AGPRs, A = V^T read transposed from LDS
-//                    (ds_read_b64_tr_b16, three ahead), B = P^T straight from the
-//                    S^T registers; one inline-assembly block that also carries the
-//                    scalar load of tile it+4's row addresses
+// Iteration i, per wave (32 keys x 32 heads per tile):
+//   wait for tile i+1, workgroup barrier
+//   S^T(i+1) = K Q^T   36 MFMA 32x32x16 into a VGPR accumulator, A = K rows from
+//                      LDS (ds_read_b128, three ahead), B = Q; the softmax of tile i
+//                      and the DMA of tile i+3 (into tile i-1's slot) are issued
+//                      between these MFMAs, so the VALU and DMA work overlaps the
+//                      matrix core
+//   softmax(i)         P = 2^(x - m) in a per-unit frame m, bf16(P)
+//   O^T += V^T P^T     32 MFMA into the AGPRs, A = V^T read transposed from LDS
+//                      (ds_read_b64_tr_b16, three ahead), B = P^T; one inline-assembly
+//                      block that also carries the scalar load of tile i+4's row
+//                      addresses
+// Tiles i (V), i+1 (K) and i+3 (landing) sit in distinct slots; tiles i+2 and i+3
+// are in flight while tile i+1 is computed.
 //
 // Row addresses: the resolve kernel turns each row code into a 64-bit pool
 // address (the shared zero row for -1).  Each wave gathers 8 rows per tile
