@@ -126,7 +126,13 @@ __device__ __forceinline__ void wait_barrier() {
 // One work unit u.  Returns true (workgroup-uniform) when the first pass must be
 // redone; m_obs then holds each lane's observed maximum (log2 units), which the
 // REDO instance takes as its frame.
-template <int DQK, int QT, bool REDO>
+// Cache policy of the gather DMA: STREAM (non-temporal loads) when every row is
+// read by one token (decode: the rows would only displace reused lines from L2 and
+// MALL), the default when nearby tokens re-read the same rows (prefill).
+template <bool STREAM>
+constexpr int gather_cpol() { return STREAM ? 2 : 0; }  // 2: the NT bit of the buffer load
+
+template <int DQK, int QT, bool STREAM, bool REDO>
 __device__ __forceinline__ bool attend_unit(
     int u, AttendLds<DQK>& sm, const SasFwdArgs& a, const uint16_t* __restrict__ q,
     const uint64_t* __restrict__ addr_list, const int* __restrict__ ncmp,
@@ -287,7 +293,7 @@ __device__ __forceinline__ bool attend_unit(
   auto dma_lat = [&](int i, const RowAddrs& ra, int k) {
     lds_u8* dst = tiles + (i & (NSTAGE - 1)) * TILEB + (8 * wu + k) * STRA;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(row_rsrc(ra[k]), (void __attribute__((address_space(3)))*)dst, 16,
-                                             k < 4 ? voffA0 : voffA1, 0, 0, 0);
+                                             k < 4 ? voffA0 : voffA1, 0, 0, gather_cpol<STREAM>());
   };
   // Rope: lanes 0..7 copy the 128-B rope of one row per instruction, chunk
   // l ^ swz_b(8 w + k) = l ^ ((4 w + (k >> 1)) & 7) into slot l.  It runs after every
@@ -304,7 +310,7 @@ __device__ __forceinline__ bool attend_unit(
         for (int k = 0; k < 8; ++k)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               row_rsrc(ra[k]), (void __attribute__((address_space(3)))*)(dst + k * ROWR), 16,
-              ROWA + (vb ^ (16u * (uint32_t)((4 * wu + (k >> 1)) & 7))), 0, 0, 0);
+              ROWA + (vb ^ (16u * (uint32_t)((4 * wu + (k >> 1)) & 7))), 0, 0, gather_cpol<STREAM>());
       }
     }
   };
@@ -664,7 +670,7 @@ __device__ __forceinline__ bool attend_unit(
 namespace sas {
 
 // One workgroup per work unit.
-template <int DQK, int QT>
+template <int DQK, int QT, bool STREAM>
 __global__ __launch_bounds__(256, 1) void attend_kernel(
     SasFwdArgs a, const uint16_t* __restrict__ q, const uint8_t* __restrict__ ori_kv,
     const uint8_t* __restrict__ cmp_kv, const int* __restrict__ cmp_bt,
@@ -675,10 +681,10 @@ __global__ __launch_bounds__(256, 1) void attend_kernel(
   const int u = blockIdx.x;
   if (plan[PH_MAGIC] != SAS_PLAN_MAGIC || u >= plan[PH_UNITS]) return;
   float m_obs = 0.f;
-  if (attend_unit<DQK, QT, false>(u, sm, a, q, addr_list, ncmp, sinks, plan, out, lse, ws_o,
+  if (attend_unit<DQK, QT, STREAM, false>(u, sm, a, q, addr_list, ncmp, sinks, plan, out, lse, ws_o,
                                   ws_ml, m_obs)) {
     lds_barrier();  // every wave is done with the ring before the redo refills it
-    attend_unit<DQK, QT, true>(u, sm, a, q, addr_list, ncmp, sinks, plan, out, lse, ws_o, ws_ml,
+    attend_unit<DQK, QT, STREAM, true>(u, sm, a, q, addr_list, ncmp, sinks, plan, out, lse, ws_o, ws_ml,
                                m_obs);
   }
 }

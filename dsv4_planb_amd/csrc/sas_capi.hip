@@ -153,11 +153,19 @@ typedef void (*attend_fn_t)(SasFwdArgs, const uint16_t*, const uint8_t*, const u
                             const int*, const uint64_t*, const int*, const float*, const int*,
                             uint16_t*, float*, float*, float*);
 
+template <int DQK, bool NT>
+attend_fn_t attend_ptr(bool f16) {
+  return f16 ? &sas::attend_kernel<DQK, 1, NT> : &sas::attend_kernel<DQK, 0, NT>;
+}
+
+// Decode-like calls (at most 4 query tokens per sequence on average) read each KV
+// row for one token only: their gather uses non-temporal loads.  Prefill-like calls,
+// where nearby tokens share most of their rows, keep the default cache policy.
 attend_fn_t pick_attend(const sas_params_t* p) {
   const bool f16 = p->q_dtype == SAS_DT_FP16;
-  if (p->head_dim_qk == 576)
-    return f16 ? &sas::attend_kernel<576, 1> : &sas::attend_kernel<576, 0>;
-  return f16 ? &sas::attend_kernel<512, 1> : &sas::attend_kernel<512, 0>;
+  const bool nt = (int64_t)p->total_tokens <= 4 * (int64_t)p->batch;
+  if (p->head_dim_qk == 576) return nt ? attend_ptr<576, true>(f16) : attend_ptr<576, false>(f16);
+  return nt ? attend_ptr<512, true>(f16) : attend_ptr<512, false>(f16);
 }
 
 int launch_status() { return hipGetLastError() == hipSuccess ? SAS_OK : SAS_ERR_LAUNCH; }
