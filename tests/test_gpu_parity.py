@@ -325,3 +325,65 @@ def test_device_plan_covers_every_row_once(cores):
                 assert tok[t, 7] == -1 and t not in stoks
     assert not by_tok, f"units for tokens no batch owns: {list(by_tok)[:5]}"
     assert (used == 1).all(), "split workspace slots overlap or go unused"
+
+
+# ---- hipGraph capture (reference test_graph_mode.py:107-209) ----
+@pytest.mark.parametrize("with_plan", [False, True])
+def test_graph_replays_match_eager(with_plan):
+    """The captured forward (planner inside the graph or a plan passed in; many
+    split tokens, so the combine pass is in the graph too) replayed several times,
+    with other eager work and host syncs between the replays: every replay equals
+    the eager call bit for bit, also after the query is refreshed in place."""
+    from dsv4_planb_amd import metadata as M
+    from dsv4_planb_amd.api import build_launch
+    from dsv4_planb_amd.graph import SasGraph
+
+    c = make_case(B=3, H=64, seq_kv=[20000, 3000, 9000], q_per_seq=[2, 1, 3], scenario=3, K=1024,
+                  seed=21)
+    _banner(f"graph plan={with_plan}", c)
+    d = to_device(c)
+    cu = d["cu_seqlens_q"]
+    plan = None
+    if with_plan:
+        plan = M.sparse_attn_sharedkv_metadata(
+            num_heads_q=c.H, num_heads_kv=1, head_dim=576, cu_seqlens_q=cu, seqused_kv=d["seqused_kv"],
+            batch_size=c.B, max_seqlen_q=3, max_seqlen_kv=20000, cmp_topk=c.K, cmp_ratio=4,
+            layout_q="TND", has_cmp_kv=True, aic_core_num=1024)
+    launch, out, lse = build_launch(
+        q_flat=d["q"], ori_kv=d["ori_kv"], ori_block_table=d["ori_block_table"],
+        cmp_kv=d["cmp_kv"], cmp_block_table=d["cmp_block_table"],
+        cmp_indices=d["cmp_sparse_indices"], q_prefix=cu[:-1], act_q_lens=cu[1:] - cu[:-1],
+        seqused_kv=d["seqused_kv"], sinks=d["sinks"], metadata=plan, scenario=3, topk=c.K,
+        cmp_ratio=4, ori_win_left=127, softmax_scale=c.softmax_scale, core_num=1024)
+    launch.run()
+    torch.cuda.synchronize()
+    ref_out, ref_lse = out.clone(), lse.clone()
+    oc, lc = c.oracle_c()
+    assert_parity(out.float().cpu().numpy(), lse.cpu().numpy(), oc, lc, label="graph-eager")
+    graph = SasGraph(launch)
+    try:
+        for k in range(3):
+            out.zero_()
+            lse.fill_(float("nan"))
+            junk = torch.randn(1 << 16, device="cuda").sum()  # other eager work between replays
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref_out), f"replay {k}: output differs from the eager call"
+            assert torch.equal(lse, ref_lse), f"replay {k}: lse differs from the eager call"
+            del junk
+        # new query values written into the captured tensor
+        d["q"].copy_(torch.flip(d["q"], dims=[1]))
+        launch.run()
+        torch.cuda.synchronize()
+        ref2_out, ref2_lse = out.clone(), lse.clone()
+        assert not torch.equal(ref2_out, ref_out)
+        for k in range(2):
+            out.zero_()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref2_out), f"refreshed replay {k}: output differs"
+            assert torch.equal(lse, ref2_lse), f"refreshed replay {k}: lse differs"
+    finally:
+        graph.close()
