@@ -227,6 +227,8 @@ __device__ __forceinline__ int paged_code(const int* __restrict__ bt_row, int ta
 constexpr int RS_NT = 256;
 constexpr int RS_PER = 8;  // index slots per thread and chunk
 
+constexpr int RS_CBT_LDS = 4096;  // compressed block-table entries staged in LDS
+
 __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int* __restrict__ plan,
                                                         const int* __restrict__ ori_bt,
                                                         const int* __restrict__ idx,
@@ -239,9 +241,33 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
                                                         int esz) {
   __shared__ int s_wmin[RS_NT / 64];
   __shared__ int s_wsum[RS_NT / 64];
+  __shared__ int s_cbt[RS_CBT_LDS];
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
+  const int* ir = idx + (size_t)t * a.K;
+  const bool vec = (a.K & 3) == 0;  // index rows are 16-B aligned
+  // Index slots [s0, s0 + RS_PER) below `bound`, all loaded before any is used
+  // (-2: past the bound).
+  auto load_slots = [&](int (&v)[RS_PER], int s0, int bound) {
+    if (vec && s0 + RS_PER <= bound) {
+#pragma unroll
+      for (int k = 0; k < RS_PER; k += 4) {
+        const int4 x = *reinterpret_cast<const int4*>(ir + s0 + k);
+        v[k] = x.x;
+        v[k + 1] = x.y;
+        v[k + 2] = x.z;
+        v[k + 3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < RS_PER; ++k) v[k] = s0 + k < bound ? ir[s0 + k] : -2;
+    }
+  };
+  // First memory round trip: the token's plan record and, independent of it, the
+  // first pass of its index slots.
+  int v0[RS_PER];
+  if (a.scenario == 3) load_slots(v0, tid * RS_PER, a.K);
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
   const int b = tk[TK_B];
   if (b < 0) {
@@ -251,6 +277,12 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
   int* out = rows_out + (size_t)t * a.list_stride;
   uint64_t* aout = addr_out + (size_t)t * a.list_stride;
   const int nwin = tk[TK_NWIN], winlo = tk[TK_WINLO];
+  // Second: the window's block-table entries and the batch's compressed block-table
+  // row, staged in LDS so the per-id page lookups below stay on chip.
+  const int* cbt_g = cmp_bt + (size_t)b * a.cmp_table_len;
+  const bool cbt_lds = a.scenario >= 2 && a.cmp_table_len <= RS_CBT_LDS;
+  if (cbt_lds)
+    for (int i = tid; i < a.cmp_table_len; i += RS_NT) s_cbt[i] = cbt_g[i];
   const int* obt = ori_bt + (size_t)b * a.ori_table_len;
   for (int r = tid; r < nwin; r += RS_NT) {
     const int code = paged_code(obt, a.ori_table_len, a.ori_block_size, a.ori_block_num, winlo + r);
@@ -262,13 +294,14 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     if (tid == 0) ncmp_out[t] = 0;
     return;
   }
+  __syncthreads();  // s_cbt
+  const int* cbt = cbt_lds ? s_cbt : cbt_g;
   out += nwin;  // compressed codes follow the window codes
   const int thr = floor_div(tk[TK_SG] + 1, a.cmp_ratio);
   if (a.scenario == 2) {  // golden.py:146-150: every compressed row below thr
     const int n = max(min(thr, a.K), 0);
-    const int* cbt2 = cmp_bt + (size_t)b * a.cmp_table_len;
     for (int j = tid; j < n; j += RS_NT) {
-      const int code = paged_code(cbt2, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, j);
+      const int code = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, j);
       out[j] = code;
       aout[j] = code_addr(code, cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
     }
@@ -276,29 +309,18 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     return;
   }
   const int limit = max(min(a.K, thr), 0);  // golden.py:48
-  const int* ir = idx + (size_t)t * a.K;
-  const int* cbt = cmp_bt + (size_t)b * a.cmp_table_len;
-  // Chunks of RS_NT * RS_PER slots; thread tid owns slots [RS_PER tid, RS_PER (tid + 1))
-  // of a chunk and loads them all before using any (one memory round trip), then
-  // the terminator, the survivors and their slot-order positions come from
-  // block-wide reductions over registers.
-  const bool vec = (a.K & 3) == 0;  // index rows are 16-B aligned
-  int emitted = 0;                  // compressed rows written so far (block-uniform)
+  // Passes of RS_NT * RS_PER slots; thread tid owns slots [RS_PER tid, RS_PER (tid + 1))
+  // of a pass; the terminator, the survivors and their slot-order positions come
+  // from block-wide reductions over registers.
+  int emitted = 0;  // compressed rows written so far (block-uniform)
   for (int c0 = 0; c0 < limit; c0 += RS_NT * RS_PER) {
     const int s0 = c0 + tid * RS_PER;
     int v[RS_PER];
-    if (vec && s0 + RS_PER <= limit) {
+    if (c0 == 0) {
 #pragma unroll
-      for (int k = 0; k < RS_PER; k += 4) {
-        const int4 x = *reinterpret_cast<const int4*>(ir + s0 + k);
-        v[k] = x.x;
-        v[k + 1] = x.y;
-        v[k + 2] = x.z;
-        v[k + 3] = x.w;
-      }
+      for (int k = 0; k < RS_PER; ++k) v[k] = s0 + k < limit ? v0[k] : -2;
     } else {
-#pragma unroll
-      for (int k = 0; k < RS_PER; ++k) v[k] = s0 + k < limit ? ir[s0 + k] : -2;
+      load_slots(v, s0, limit);
     }
     // golden.py:52-53: the first -1 terminates the list
     int first = limit;
@@ -344,7 +366,8 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
         aout[pos++] = code_addr(code, cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
       }
     emitted += total;
-    if (term < limit) break;  // the list ended in this chunk
+    if (term < limit) break;  // the list ended in this pass
+    __syncthreads();          // s_wmin / s_wsum are rewritten by the next pass
   }
   if (tid == 0) ncmp_out[t] = emitted;
 }
