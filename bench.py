@@ -11,7 +11,7 @@ window 128, compression ratio 4, d_qk 576, d_v 512, scale 1/sqrt(576)):
   2048 over the causally valid compressed rows (-1 padded).  MFMA-bound.
 * ``decode32``: B=32, 64 heads, KV lengths U[4096, 32768], top-k 512.
 
-A step is one forward call (row resolution, attention, split combine) with the
+A step is one forward call (row resolution, then attention, which merges split tokens) with the
 split-KV plan built beforehand by the metadata op, replayed from a hipGraph.
 ``value`` is microseconds per call (lower is better).  ``roofline`` rates the
 attention kernel alone, timed with HIP events on the stream it runs on.
