@@ -10,8 +10,11 @@ window 128, compression ratio 4, d_qk 576, d_v 512, scale 1/sqrt(576)):
 * ``prefill8k``: one sequence, 8192 query tokens over 8192 KV, 128 heads, top-k
   2048 over the causally valid compressed rows (-1 padded).  MFMA-bound.
 * ``decode32``: B=32, 64 heads, KV lengths U[4096, 32768], top-k 512.
+* ``ragged_fp8``: B=64, KV lengths log-uniform in [256, 131072], 1, 2 or 4 query
+  tokens per sequence, 128 heads, top-k 2048 (-1 padded where fewer compressed
+  rows are valid); KV pools fp8 e4m3 with a per-row fp32 scale (580 B per row).
 
-A step is one forward call (row resolution, then attention, which merges split tokens) with the
+A step is one forward call (row resolution, attention, split combine) with the
 split-KV plan built beforehand by the metadata op, replayed from a hipGraph.
 ``value`` is microseconds per call (lower is better).  ``roofline`` rates the
 attention kernel alone, timed with HIP events on the stream it runs on.
@@ -38,6 +41,9 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 D_QK, D_V, PAGE, WIN, RATIO = 576, 512, 64, 128, 4
 ROW_BYTES = D_QK * 2
+ROW_BYTES_FP8 = D_QK + 4  # e4m3 payload + fp32 scale
+KERNEL_NAME = {"decode128k": "sas::attend_kernel<576, bf16>", "prefill8k": "sas::attend_kernel<576, bf16>",
+               "decode32": "sas::attend_kernel<576, bf16>", "ragged_fp8": "sas::fwd_kernel (fp8 e4m3 KV)"}
 FLOP_PER_ROW_HEAD = 2 * D_QK + 2 * D_V
 
 
@@ -55,29 +61,54 @@ def _random_subsets(n_tok, thr, K, space, gen, dev):
                        torch.full_like(order, -1))
 
 
+def _fp8_pool(n_pages, gen, dev):
+    """N(0, 1) rows stored as e4m3 with a per-row fp32 scale (row max -> 448)."""
+    x = torch.randn((n_pages, PAGE, 1, D_QK), dtype=torch.float32, device=dev, generator=gen)
+    sc = x.abs().amax(dim=-1).clamp(min=1e-12) / 448.0
+    return (x / sc[..., None]).to(torch.float8_e4m3fn), sc.contiguous()
+
+
 def make_workload(name: str, seed: int = 0, dev="cuda", compact: bool = False):
     """Synthetic inputs of one workload.  compact: every sequence's block tables
     point at the first sequence's pages (a KV footprint that fits the 256 MB MALL;
     for locality experiments only, never the benchmark figure)."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
+    fp8 = False
     if name == "decode128k":
         B, q_per, H, ctx, K = 128, 2, 128, 131072, 2048
         kv = [ctx] * B
+        q_lens = [q_per] * B
     elif name == "prefill8k":
         B, q_per, H, K = 1, 8192, 128, 2048
         kv = [8192]
+        q_lens = [q_per]
     elif name == "decode32":
         B, q_per, H, K = 32, 1, 64, 512
         rng = np.random.default_rng(seed)
         kv = rng.integers(4096, 32769, size=B).tolist()
+        q_lens = [q_per] * B
+    elif name == "ragged_fp8":
+        B, H, K = 64, 128, 2048
+        rng = np.random.default_rng(seed)
+        kv = np.exp(rng.uniform(np.log(256), np.log(131072), size=B)).astype(np.int64).tolist()
+        q_lens = rng.choice([1, 2, 4], size=B).tolist()
+        q_per = max(q_lens)
+        fp8 = True
     else:
         raise ValueError(name)
-    T = B * q_per
+    T = sum(q_lens)
     pages = [math.ceil(x / PAGE) for x in kv]
     cpages = [math.ceil((x // RATIO) / PAGE) for x in kv]
-    ori_pool = torch.randn((sum(pages), PAGE, 1, D_QK), dtype=torch.bfloat16, device=dev, generator=gen)
-    cmp_pool = torch.randn((sum(cpages), PAGE, 1, D_QK), dtype=torch.bfloat16, device=dev, generator=gen)
+    ori_scale = cmp_scale = None
+    if fp8:
+        ori_pool, ori_scale = _fp8_pool(sum(pages), gen, dev)
+        cmp_pool, cmp_scale = _fp8_pool(sum(cpages), gen, dev)
+    else:
+        ori_pool = torch.randn((sum(pages), PAGE, 1, D_QK), dtype=torch.bfloat16, device=dev,
+                               generator=gen)
+        cmp_pool = torch.randn((sum(cpages), PAGE, 1, D_QK), dtype=torch.bfloat16, device=dev,
+                               generator=gen)
     perm = torch.randperm(sum(pages), device=dev, generator=gen).to(torch.int32)
     cperm = torch.randperm(sum(cpages), device=dev, generator=gen).to(torch.int32)
     obt = torch.full((B, max(pages)), -1, dtype=torch.int32, device=dev)
@@ -93,32 +124,56 @@ def make_workload(name: str, seed: int = 0, dev="cuda", compact: bool = False):
         cbt[:, :] = cbt[0:1, :].clone()
     q = torch.randn((T, H, D_QK), dtype=torch.bfloat16, device=dev, generator=gen)
     sinks = (torch.rand(H, device=dev, generator=gen) * 2 - 1).float()
-    cu = torch.arange(0, T + 1, q_per, dtype=torch.int32, device=dev)
+    qlen = torch.tensor(q_lens, dtype=torch.int32, device=dev)
+    cu = torch.zeros(B + 1, dtype=torch.int32, device=dev)
+    cu[1:] = torch.cumsum(qlen, 0)
     seqused = torch.tensor(kv, dtype=torch.int32, device=dev)
-    b_of = torch.arange(T, device=dev) // q_per
-    s_loc = torch.arange(T, device=dev) % q_per
-    s_g = seqused[b_of] - q_per + s_loc
+    b_of = torch.repeat_interleave(torch.arange(B, device=dev), qlen.long())
+    s_loc = torch.arange(T, device=dev) - cu[b_of]
+    s_g = seqused[b_of] - qlen[b_of] + s_loc
     thr = torch.div(s_g + 1, RATIO, rounding_mode="floor")
     space = int((max(kv) // RATIO))
     idx = _random_subsets(T, thr, K, space, gen, dev).reshape(T, 1, K)
     n_win = (s_g + 1 - torch.clamp(s_g - (WIN - 1), min=0)).clamp(min=0)
     n_cmp = torch.clamp(thr, min=0, max=K)
     # algorithmic work: unique KV rows per sequence, FLOPs per (row, head)
-    uniq = 0
-    ids = torch.where(idx.reshape(B, q_per * K) >= 0, idx.reshape(B, q_per * K),
-                      torch.full_like(idx.reshape(B, q_per * K), -1))
-    srt = torch.sort(ids, dim=1).values
-    distinct = ((srt[:, 1:] != srt[:, :-1]) & (srt[:, 1:] >= 0)).sum(1) + (srt[:, 0] >= 0).long()
-    win_lo = torch.clamp(s_g - (WIN - 1), min=0).reshape(B, q_per).min(1).values
-    win_hi = s_g.reshape(B, q_per).max(1).values
-    uniq = int(distinct.sum().item() + (win_hi - win_lo + 1).clamp(min=0).sum().item())
+    flat = idx.reshape(T, K).long()
+    keyed = torch.where(flat >= 0, b_of[:, None].long() * (space + 1) + flat, torch.full_like(flat, -1))
+    distinct = int(torch.unique(keyed[keyed >= 0]).numel())
+    win_lo = torch.full((B,), 1 << 40, dtype=torch.long, device=dev).scatter_reduce(
+        0, b_of, torch.clamp(s_g - (WIN - 1), min=0).long(), reduce="amin")
+    win_hi = torch.full((B,), -1, dtype=torch.long, device=dev).scatter_reduce(
+        0, b_of, s_g.long(), reduce="amax")
+    uniq = distinct + int((win_hi - win_lo + 1).clamp(min=0).sum().item())
     rows_total = int((n_win + n_cmp).sum().item())
-    alg_bytes = (T * H * D_QK * 2 + T * H * D_V * 2 + T * H * 4 + T * K * 4 + uniq * ROW_BYTES)
+    alg_bytes = (T * H * D_QK * 2 + T * H * D_V * 2 + T * H * 4 + T * K * 4 +
+                 uniq * (ROW_BYTES_FP8 if fp8 else ROW_BYTES))
     alg_flops = rows_total * H * FLOP_PER_ROW_HEAD
     return dict(name=name, B=B, T=T, H=H, K=K, q_per=q_per, kv=kv, q=q, ori_kv=ori_pool,
-                cmp_kv=cmp_pool, ori_bt=obt, cmp_bt=cbt, idx=idx, sinks=sinks, cu=cu,
-                seqused=seqused, alg_bytes=alg_bytes, alg_flops=alg_flops, uniq_rows=uniq,
-                rows_total=rows_total)
+                cmp_kv=cmp_pool, ori_scale=ori_scale, cmp_scale=cmp_scale, ori_bt=obt, cmp_bt=cbt,
+                idx=idx, sinks=sinks, cu=cu, seqused=seqused, alg_bytes=alg_bytes,
+                alg_flops=alg_flops, uniq_rows=uniq, rows_total=rows_total, fp8=fp8)
+
+
+def build_call(wl, core_num=256):
+    """The metadata op's plan and a launch object for one workload: (plan, launch, out, lse)."""
+    from dsv4_planb_amd import metadata as M
+    from dsv4_planb_amd.api import build_launch
+
+    cu = wl["cu"]
+    plan = M.sparse_attn_sharedkv_metadata(
+        num_heads_q=wl["H"], num_heads_kv=1, head_dim=D_QK, cu_seqlens_q=cu,
+        seqused_kv=wl["seqused"], batch_size=wl["B"], max_seqlen_q=wl["q_per"],
+        max_seqlen_kv=max(wl["kv"]), cmp_topk=wl["K"], cmp_ratio=RATIO, layout_q="TND",
+        has_cmp_kv=True, aic_core_num=core_num)
+    launch, out, lse = build_launch(
+        q_flat=wl["q"], ori_kv=wl["ori_kv"], ori_block_table=wl["ori_bt"], cmp_kv=wl["cmp_kv"],
+        cmp_block_table=wl["cmp_bt"], cmp_indices=wl["idx"], q_prefix=cu[:-1],
+        act_q_lens=cu[1:] - cu[:-1], seqused_kv=wl["seqused"], sinks=wl["sinks"],
+        metadata=plan, scenario=3, topk=wl["K"], cmp_ratio=RATIO, ori_win_left=WIN - 1,
+        softmax_scale=1.0 / math.sqrt(D_QK), core_num=core_num, ori_kv_scale=wl["ori_scale"],
+        cmp_kv_scale=wl["cmp_scale"])
+    return plan, launch, out, lse
 
 
 # ---------------------------------------------------------------------------
@@ -140,9 +195,7 @@ def _events_time(fn, n, stream):
 
 
 def measure(wl, steps, warmup, core_num=256):
-    from dsv4_planb_amd import metadata as M
     from dsv4_planb_amd import sparse_attn_sharedkv
-    from dsv4_planb_amd.api import build_launch
     from dsv4_planb_amd.graph import SasGraph
 
     dev = wl["q"].device
@@ -150,20 +203,10 @@ def measure(wl, steps, warmup, core_num=256):
     stream = torch.cuda.Stream(device=dev)  # all timed work runs on this stream
     with torch.cuda.stream(stream):
         t0 = time.perf_counter()
-        plan = M.sparse_attn_sharedkv_metadata(
-            num_heads_q=wl["H"], num_heads_kv=1, head_dim=D_QK, cu_seqlens_q=wl["cu"],
-            seqused_kv=wl["seqused"], batch_size=wl["B"], max_seqlen_q=wl["q_per"],
-            max_seqlen_kv=max(wl["kv"]), cmp_topk=wl["K"], cmp_ratio=RATIO, layout_q="TND",
-            has_cmp_kv=True, aic_core_num=core_num)
+        plan, launch, out, lse = build_call(wl, core_num)
         torch.cuda.synchronize()
-        plan_host_us = (time.perf_counter() - t0) * 1e6
+        plan_host_us = (time.perf_counter() - t0) * 1e6  # metadata op + launch set-up
         cu = wl["cu"]
-        launch, out, lse = build_launch(
-            q_flat=wl["q"], ori_kv=wl["ori_kv"], ori_block_table=wl["ori_bt"], cmp_kv=wl["cmp_kv"],
-            cmp_block_table=wl["cmp_bt"], cmp_indices=wl["idx"], q_prefix=cu[:-1],
-            act_q_lens=cu[1:] - cu[:-1], seqused_kv=wl["seqused"], sinks=wl["sinks"],
-            metadata=plan, scenario=3, topk=wl["K"], cmp_ratio=RATIO, ori_win_left=WIN - 1,
-            softmax_scale=scale, core_num=core_num)
         for _ in range(max(warmup, 1)):
             launch.run()
         torch.cuda.synchronize()
@@ -186,7 +229,8 @@ def measure(wl, steps, warmup, core_num=256):
         api_kw = dict(ori_kv=wl["ori_kv"], cmp_kv=wl["cmp_kv"], cmp_sparse_indices=wl["idx"],
                       ori_block_table=wl["ori_bt"], cmp_block_table=wl["cmp_bt"], cu_seqlens_q=cu,
                       seqused_kv=wl["seqused"], sinks=wl["sinks"], metadata=plan,
-                      softmax_scale=scale, cmp_ratio=RATIO, topk_cmp=wl["K"])
+                      softmax_scale=scale, cmp_ratio=RATIO, topk_cmp=wl["K"],
+                      ori_kv_scale=wl["ori_scale"], cmp_kv_scale=wl["cmp_scale"])
         sparse_attn_sharedkv(wl["q"], **api_kw)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
@@ -353,22 +397,8 @@ def cpu_baseline(name, n_seq, seed=0):
 def profile_attend(name, steps, dev, core_num=256):
     """Plan and resolve once, then launch only the attention stage `steps` times
     (the kernel the roofline rates), for rocprofv3 counter runs."""
-    from dsv4_planb_amd import metadata as M
-    from dsv4_planb_amd.api import build_launch
-
     wl = make_workload(name, seed=0, dev=dev)
-    cu = wl["cu"]
-    plan = M.sparse_attn_sharedkv_metadata(
-        num_heads_q=wl["H"], num_heads_kv=1, head_dim=D_QK, cu_seqlens_q=cu,
-        seqused_kv=wl["seqused"], batch_size=wl["B"], max_seqlen_q=wl["q_per"],
-        max_seqlen_kv=max(wl["kv"]), cmp_topk=wl["K"], cmp_ratio=RATIO, layout_q="TND",
-        has_cmp_kv=True, aic_core_num=core_num)
-    launch, out, lse = build_launch(
-        q_flat=wl["q"], ori_kv=wl["ori_kv"], ori_block_table=wl["ori_bt"], cmp_kv=wl["cmp_kv"],
-        cmp_block_table=wl["cmp_bt"], cmp_indices=wl["idx"], q_prefix=cu[:-1],
-        act_q_lens=cu[1:] - cu[:-1], seqused_kv=wl["seqused"], sinks=wl["sinks"],
-        metadata=plan, scenario=3, topk=wl["K"], cmp_ratio=RATIO, ori_win_left=WIN - 1,
-        softmax_scale=1.0 / math.sqrt(D_QK), core_num=core_num)
+    _, launch, _, _ = build_call(wl, core_num)
     launch.run("resolve")
     for _ in range(steps):
         launch.run("attend")
@@ -424,22 +454,8 @@ def power_mode(name, secs, dev, compact=False):
                                             ctypes.c_size_t(4 << 30), ctypes.c_void_p(out.data_ptr()),
                                             2048, sp)
     else:
-        from dsv4_planb_amd import metadata as M
-        from dsv4_planb_amd.api import build_launch
-
         wl = make_workload(name, seed=0, dev=dev, compact=compact)
-        cu = wl["cu"]
-        plan = M.sparse_attn_sharedkv_metadata(
-            num_heads_q=wl["H"], num_heads_kv=1, head_dim=D_QK, cu_seqlens_q=cu,
-            seqused_kv=wl["seqused"], batch_size=wl["B"], max_seqlen_q=wl["q_per"],
-            max_seqlen_kv=max(wl["kv"]), cmp_topk=wl["K"], cmp_ratio=RATIO, layout_q="TND",
-            has_cmp_kv=True, aic_core_num=256)
-        launch, _, _ = build_launch(
-            q_flat=wl["q"], ori_kv=wl["ori_kv"], ori_block_table=wl["ori_bt"], cmp_kv=wl["cmp_kv"],
-            cmp_block_table=wl["cmp_bt"], cmp_indices=wl["idx"], q_prefix=cu[:-1],
-            act_q_lens=cu[1:] - cu[:-1], seqused_kv=wl["seqused"], sinks=wl["sinks"],
-            metadata=plan, scenario=3, topk=wl["K"], cmp_ratio=RATIO, ori_win_left=WIN - 1,
-            softmax_scale=1.0 / math.sqrt(D_QK), core_num=256)
+        _, launch, _, _ = build_call(wl)
         launch.run("resolve")
         fn = lambda: launch.run("attend")  # noqa: E731
     idle = _smi_sample()
@@ -465,7 +481,7 @@ def power_mode(name, secs, dev, compact=False):
 
 
 def main_r_batch(name):
-    return dict(decode128k=128, decode32=32, prefill8k=1)[name]
+    return dict(decode128k=128, decode32=32, prefill8k=1, ragged_fp8=64)[name]
 
 
 # ---------------------------------------------------------------------------
@@ -475,8 +491,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="decode128k",
-                    choices=["decode128k", "prefill8k", "decode32"])
-    ap.add_argument("--extra", default="prefill8k,decode32",
+                    choices=["decode128k", "prefill8k", "decode32", "ragged_fp8"])
+    ap.add_argument("--extra", default="prefill8k,decode32,ragged_fp8",
                     help="comma-separated extra workloads reported under 'workloads' ('' = none)")
     ap.add_argument("--cpu-seqs", type=int, default=0,
                     help="cap on sampled sequences for the CPU baseline (0 = size for ~10 s)")
@@ -489,7 +505,8 @@ def main():
                          "--steps times (calibrates the HBM byte counters); power: --stage back "
                          "to back for --secs with a power / clock sample")
     ap.add_argument("--stage", default="decode128k",
-                    choices=["decode128k", "prefill8k", "decode32", "mfma_probe", "read_probe"],
+                    choices=["decode128k", "prefill8k", "decode32", "ragged_fp8", "mfma_probe",
+                             "read_probe"],
                     help="what --mode power runs")
     ap.add_argument("--secs", type=float, default=10.0, help="--mode power duration")
     ap.add_argument("--compact", action="store_true",
@@ -557,10 +574,10 @@ def main():
                 "frac": round(ach / peak, 4), "traffic": _traffic_from_profile(args.workload),
                 "measured_peak": measured,
                 "frac_of_measured": round(ach / measured, 4) if measured else None,
-                "kernel": "sas::attend_kernel<576, bf16>", "kernel_us": round(main_r["attend_us"], 2),
+                "kernel": KERNEL_NAME[args.workload], "kernel_us": round(main_r["attend_us"], 2),
                 "algorithmic_bytes": main_r["alg_bytes"], "algorithmic_flops": main_r["alg_flops"]}
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.workload != "ragged_fp8":
         _log("cpu baseline")
         if args.workload == "prefill8k":
             cpu = cpu_baseline(args.workload, 1)
@@ -576,6 +593,9 @@ def main():
                      "window 128, ratio 4, page 64, d_qk 576 / d_v 512",
         "decode32": "decode: B=32 seqs x U[4096,32768] KV, 1 query token, H=64, top-k 512, "
                     "window 128, ratio 4, page 64, d_qk 576 / d_v 512",
+        "ragged_fp8": "ragged: B=64 seqs x log-U[256,131072] KV, 1/2/4 query tokens/seq, H=128, "
+                      "top-k 2048 (-1 padded), window 128, ratio 4, page 64, fp8 e4m3 KV with "
+                      "per-row fp32 scale, bf16 q",
     }
     line = {
         "metric": "us/call of the sparse shared-KV attention forward (1x MI355X), with achieved "

@@ -84,8 +84,7 @@ template <int DQK>
 struct AttendLds {
   static constexpr int TILEB = SAS_TILE * (1024 + 64) + SAS_TILE * (DQK - 512) * 2;
   uint8_t tiles[4 * TILEB];
-  int far;   // a logit of some head outgrew the frame
-  int last;  // this unit is the last split of its token to finish
+  int far;  // a logit of some head outgrew the frame
 };
 
 // d = a b^T + 0 / d += a b^T in VGPRs (the O accumulator owns the AGPRs).  Written as
@@ -138,8 +137,7 @@ __device__ __forceinline__ bool attend_unit(
     int u, AttendLds<DQK>& sm, const SasFwdArgs& a, const uint16_t* __restrict__ q,
     const uint64_t* __restrict__ addr_list, const int* __restrict__ ncmp,
     const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
-    float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    int* __restrict__ split_cnt, float& m_obs) {
+    float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml, float& m_obs) {
   constexpr int DV = 512;
   constexpr int NT = 256;
   constexpr int TILE = SAS_TILE;          // 32 keys
@@ -226,10 +224,9 @@ __device__ __forceinline__ bool attend_unit(
   // the sink's alone.  Returning here also keeps the accumulators below on a
   // single path, so the epilogue does not have to merge them with zeros.
   if (ntiles == 0) {
-    if (REDO) return false;  // (never happens: a redo needs rows)
+    if (REDO || !hvalid) return false;  // (a redo always has rows)
     const float l_sink = split == 0 ? 1.f : 0.f;
     if (splits == 1) {
-      if (!hvalid) return false;
       uint16_t* orow = out + ((size_t)t * H + h) * DV + 16 * g;
 #pragma unroll
       for (int mb = 0; mb < 16; ++mb)
@@ -238,18 +235,15 @@ __device__ __forceinline__ bool attend_unit(
           *reinterpret_cast<u32x4_t*>(orow + 32 * mb + 8 * hf) = u32x4_t{0, 0, 0, 0};
       if (lse && g == 0) lse[(size_t)t * H + h] = (sink2 + __log2f(l_sink)) * 0.6931471805599453f;
     } else {
-      if (hvalid) {
-        const int slot = wsbase + split;
-        float* orow = ws_o + ((size_t)slot * H + h) * DV + 16 * g;
+      const int slot = wsbase + split;
+      float* orow = ws_o + ((size_t)slot * H + h) * DV + 16 * g;
 #pragma unroll
-        for (int mb = 0; mb < 16; ++mb)
+      for (int mb = 0; mb < 16; ++mb)
 #pragma unroll
-          for (int qd = 0; qd < 4; ++qd)
-            *reinterpret_cast<float4*>(orow + 32 * mb + 4 * qd) = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (g == 0)
-          reinterpret_cast<float4*>(ws_ml)[(size_t)slot * H + h] = make_float4(sink2, l_sink, l_sink, 0.f);
-      }
-      split_finish<QT>(t, H, splits, wsbase, split_cnt, sm.last, ws_o, ws_ml, out, lse);
+        for (int qd = 0; qd < 4; ++qd)
+          *reinterpret_cast<float4*>(orow + 32 * mb + 4 * qd) = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (g == 0)
+        reinterpret_cast<float4*>(ws_ml)[(size_t)slot * H + h] = make_float4(sink2, l_sink, l_sink, 0.f);
     }
     return false;
   }
@@ -629,8 +623,8 @@ __device__ __forceinline__ bool attend_unit(
   }
 
   // ---- epilogue: lane (li, g) holds d = 32 mb + 16 g + r of head li ----
+  if (!hvalid) return false;
   if (splits == 1) {
-    if (!hvalid) return false;
     const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
     uint16_t* orow = out + ((size_t)t * H + h) * DV + 16 * g;
     // One 16-register block at a time into VGPRs (the pin keeps the copies in
@@ -650,27 +644,23 @@ __device__ __forceinline__ bool attend_unit(
       }
     }
     if (lse && g == 0) lse[(size_t)t * H + h] = (m_run + __log2f(l_e)) * 0.6931471805599453f;
-  } else {
-    if (hvalid) {
-      const int slot = wsbase + split;
-      float* orow = ws_o + ((size_t)slot * H + h) * DV + 16 * g;
+  } else {  // an un-normalised partial (O, m, l_w, l_e) for the combine pass
+    const int slot = wsbase + split;
+    float* orow = ws_o + ((size_t)slot * H + h) * DV + 16 * g;
 #pragma unroll
-      for (int mb = 0; mb < 16; ++mb) {
+    for (int mb = 0; mb < 16; ++mb) {
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          float4 v;
-          v.x = acc[mb][4 * qd + 0];
-          v.y = acc[mb][4 * qd + 1];
-          v.z = acc[mb][4 * qd + 2];
-          v.w = acc[mb][4 * qd + 3];
-          *reinterpret_cast<float4*>(orow + 32 * mb + 4 * qd) = v;
-        }
+      for (int qd = 0; qd < 4; ++qd) {
+        float4 v;
+        v.x = acc[mb][4 * qd + 0];
+        v.y = acc[mb][4 * qd + 1];
+        v.z = acc[mb][4 * qd + 2];
+        v.w = acc[mb][4 * qd + 3];
+        *reinterpret_cast<float4*>(orow + 32 * mb + 4 * qd) = v;
       }
-      if (g == 0)
-        reinterpret_cast<float4*>(ws_ml)[(size_t)slot * H + h] = make_float4(m_run, l_w, l_e, 0.f);
     }
-    // the last split of the token to finish merges the partials
-    split_finish<QT>(t, H, splits, wsbase, split_cnt, sm.last, ws_o, ws_ml, out, lse);
+    if (g == 0)
+      reinterpret_cast<float4*>(ws_ml)[(size_t)slot * H + h] = make_float4(m_run, l_w, l_e, 0.f);
   }
   return false;
 }
@@ -686,17 +676,16 @@ __global__ __launch_bounds__(256, 1) void attend_kernel(
     const uint8_t* __restrict__ cmp_kv, const int* __restrict__ cmp_bt,
     const uint64_t* __restrict__ addr_list, const int* __restrict__ ncmp,
     const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
-    float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    int* __restrict__ split_cnt) {
+    float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   __shared__ __attribute__((aligned(16))) AttendLds<DQK> sm;
   const int u = blockIdx.x;
   if (plan[PH_MAGIC] != SAS_PLAN_MAGIC || u >= plan[PH_UNITS]) return;
   float m_obs = 0.f;
   if (attend_unit<DQK, QT, STREAM, false>(u, sm, a, q, addr_list, ncmp, sinks, plan, out, lse, ws_o,
-                                          ws_ml, split_cnt, m_obs)) {
+                                          ws_ml, m_obs)) {
     lds_barrier();  // every wave is done with the ring before the redo refills it
     attend_unit<DQK, QT, STREAM, true>(u, sm, a, q, addr_list, ncmp, sinks, plan, out, lse, ws_o,
-                                       ws_ml, split_cnt, m_obs);
+                                       ws_ml, m_obs);
   }
 }
 

@@ -99,7 +99,6 @@ struct Ws {
   int* rows;
   uint64_t* addr;
   int* ncmp;
-  int* cnt;
   int* plan;
   float* o;
   float* ml;
@@ -115,7 +114,6 @@ int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out)
   out->rows = reinterpret_cast<int*>(base + W.off_rows);
   out->addr = reinterpret_cast<uint64_t*>(base + W.off_addr);
   out->ncmp = reinterpret_cast<int*>(base + W.off_ncmp);
-  out->cnt = reinterpret_cast<int*>(base + W.off_cnt);
   out->plan = reinterpret_cast<int*>(base + W.off_plan);
   out->o = reinterpret_cast<float*>(base + W.off_o);
   out->ml = reinterpret_cast<float*>(base + W.off_ml);
@@ -124,8 +122,7 @@ int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out)
 
 typedef void (*fwd_fn_t)(SasFwdArgs, const uint16_t*, const uint8_t*, const uint8_t*,
                          const float*, const float*, const int*, const int*, const int*,
-                         const int*, const float*, const int*, uint16_t*, float*, float*, float*,
-                         int*);
+                         const int*, const float*, const int*, uint16_t*, float*, float*, float*);
 
 template <int NW, int DQK, int QT, bool KV8>
 fwd_fn_t fwd_ptr() {
@@ -154,7 +151,7 @@ fwd_fn_t pick_fwd(const sas_params_t* p) {
 
 typedef void (*attend_fn_t)(SasFwdArgs, const uint16_t*, const uint8_t*, const uint8_t*,
                             const int*, const uint64_t*, const int*, const float*, const int*,
-                            uint16_t*, float*, float*, float*, int*);
+                            uint16_t*, float*, float*, float*);
 
 template <int DQK, bool NT>
 attend_fn_t attend_ptr(bool f16) {
@@ -284,7 +281,7 @@ int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
                      (hipStream_t)stream, fwd_args(p, target), plan, t->ori_block_table,
                      t->cmp_sparse_indices, t->cmp_block_table, w.rows, w.ncmp, w.addr,
                      static_cast<const uint8_t*>(t->ori_kv), static_cast<const uint8_t*>(t->cmp_kv),
-                     p->kv_dtype == SAS_DT_FP8E4M3 ? 1 : 2, w.cnt);
+                     p->kv_dtype == SAS_DT_FP8E4M3 ? 1 : 2);
   return launch_status();
 }
 
@@ -303,8 +300,7 @@ int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pla
     hipLaunchKernelGGL(pick_attend(p), dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream, a,
                        static_cast<const uint16_t*>(t->q), static_cast<const uint8_t*>(t->ori_kv),
                        static_cast<const uint8_t*>(t->cmp_kv), t->cmp_block_table, w.addr,
-                       w.ncmp, t->sinks, plan, static_cast<uint16_t*>(t->out), t->lse, w.o, w.ml,
-                       w.cnt);
+                       w.ncmp, t->sinks, plan, static_cast<uint16_t*>(t->out), t->lse, w.o, w.ml);
     return launch_status();
   }
   fwd_fn_t fn = pick_fwd(p);
@@ -312,7 +308,7 @@ int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pla
                      static_cast<const uint16_t*>(t->q), static_cast<const uint8_t*>(t->ori_kv),
                      static_cast<const uint8_t*>(t->cmp_kv), t->ori_kv_scale, t->cmp_kv_scale,
                      t->ori_block_table, t->cmp_block_table, w.rows, w.ncmp, t->sinks, plan,
-                     static_cast<uint16_t*>(t->out), t->lse, w.o, w.ml, w.cnt);
+                     static_cast<uint16_t*>(t->out), t->lse, w.o, w.ml);
   return launch_status();
 }
 
@@ -327,9 +323,11 @@ int sas_combine(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   if (!plan) plan = w.plan;
   if (p->total_tokens == 0) return SAS_OK;
   const SasFwdArgs a = fwd_args(p, target);
-  const int groups = (p->num_heads_q + sas::COMBINE_HEADS - 1) / sas::COMBINE_HEADS;
-  const dim3 grid(std::min(target * groups, 2 * std::max(1, query_num_cus())));
-  const dim3 block(64 * sas::COMBINE_HEADS);
+  // one wave per (split token, head); split tokens number fewer than `target`
+  const int waves = target * p->num_heads_q;
+  const dim3 grid(std::min((waves + sas::COMBINE_WAVES - 1) / sas::COMBINE_WAVES,
+                           2 * std::max(1, query_num_cus())));
+  const dim3 block(64 * sas::COMBINE_WAVES);
   if (p->q_dtype == SAS_DT_BF16)
     hipLaunchKernelGGL(sas::combine_kernel<0>, grid, block, 0, (hipStream_t)stream, a, plan, w.o,
                        w.ml, static_cast<uint16_t*>(t->out), t->lse);
@@ -355,8 +353,8 @@ int sas_forward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
     plan = w.plan;
   }
   if ((rc = sas_resolve(p, t, plan, ws, ws_bytes, stream))) return rc;
-  // the attention pass merges split tokens itself (the last split unit of a token)
-  return sas_attend(p, t, plan, ws, ws_bytes, stream);
+  if ((rc = sas_attend(p, t, plan, ws, ws_bytes, stream))) return rc;
+  return sas_combine(p, t, plan, ws, ws_bytes, stream);
 }
 
 int sas_debug_rows(const sas_params_t* p, const void* ws, int32_t* rows, int32_t* counts,

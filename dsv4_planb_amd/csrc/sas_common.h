@@ -54,7 +54,7 @@ SAS_HD static inline SasPlanLayout sas_plan_layout(int64_t T, int64_t target) {
 
 // ---- workspace (bytes, each region 256-B aligned) ----
 struct SasWsLayout {
-  size_t off_rows, off_addr, off_ncmp, off_cnt, off_plan, off_o, off_ml, total;
+  size_t off_rows, off_addr, off_ncmp, off_plan, off_o, off_ml, total;
   int64_t slot_cap;
 };
 
@@ -79,10 +79,6 @@ SAS_HD static inline SasWsLayout sas_ws_layout(int64_t T, int64_t K, int64_t H, 
   off = sas_align256(off + ((size_t)(T > 0 ? T : 1) * sas_row_list_stride(win_left, K, scenario) +
                             SAS_TILE) * 8);
   W.off_ncmp = off;
-  off = sas_align256(off + (size_t)(T > 0 ? T : 1) * 4);
-  // per token: split units finished so far (the last one merges the partials);
-  // zeroed by the resolve pass of every call
-  W.off_cnt = off;
   off = sas_align256(off + (size_t)(T > 0 ? T : 1) * 4);
   W.off_plan = off;
   off = sas_align256(off + (size_t)sas_plan_layout(T, target).total * 4);

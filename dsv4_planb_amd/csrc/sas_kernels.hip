@@ -238,14 +238,13 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
                                                         uint64_t* __restrict__ addr_out,
                                                         const uint8_t* __restrict__ ori_kv,
                                                         const uint8_t* __restrict__ cmp_kv,
-                                                        int esz, int* __restrict__ split_cnt) {
+                                                        int esz) {
   __shared__ int s_wmin[RS_NT / 64];
   __shared__ int s_wsum[RS_NT / 64];
   __shared__ int s_cbt[RS_CBT_LDS];
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
-  if (tid == 0) split_cnt[t] = 0;  // no split unit of this call has finished yet
   const int* ir = idx + (size_t)t * a.K;
   const bool vec = (a.K & 3) == 0;  // index rows are 16-B aligned
   // Index slots [s0, s0 + RS_PER) below `bound`, all loaded before any is used
@@ -438,6 +437,24 @@ __device__ __forceinline__ float sum2_q16(uint32_t v, float acc) {
 // of the exact P, for the LSE) in its own frame m; the merge rescales each by
 // 2^(m_s - max_s m_s).  Only split 0 carries the sink, so it enters once.
 // ===========================================================================
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// Log-sum-exp merge of the S split partials of head h of token t (partial slots
+// base .., each an un-normalised O row with its (m, l_w, l_e)), by one wave: lane
+// l owns d = 8 l .. 8 l + 7.  The partial records are read 64 at a time (lane j
+// holds record j of a chunk), and partial rows are loaded 8 at a time before any
+// is accumulated, so a merge costs a few memory round trips for any S.
+constexpr int COMBINE_BATCH = 8;
+
 template <int QT>
 __device__ __forceinline__ void combine_head(int t, int h, int H, int S, int base,
                                              const float* __restrict__ ws_o,
@@ -446,21 +463,42 @@ __device__ __forceinline__ void combine_head(int t, int h, int H, int S, int bas
   constexpr int DV = 512;
   const int lane = threadIdx.x & 63;
   const float4* ml = reinterpret_cast<const float4*>(ws_ml);
-  float mx = -INFINITY;
-  for (int s = 0; s < S; ++s) mx = fmaxf(mx, ml[(size_t)(base + s) * H + h].x);
+  auto record = [&](int s0) {
+    return s0 + lane < S ? ml[(size_t)(base + s0 + lane) * H + h] : make_float4(-INFINITY, 0.f, 0.f, 0.f);
+  };
+  const float4 rec0 = record(0);
+  float mx = rec0.x;
+  for (int s0 = 64; s0 < S; s0 += 64) mx = fmaxf(mx, record(s0).x);
+  mx = wave_max(mx);  // the merged frame
   float l = 0.f, le = 0.f;
   float4 o0 = make_float4(0.f, 0.f, 0.f, 0.f), o1 = o0;
-  for (int s = 0; s < S; ++s) {
-    const size_t row = (size_t)(base + s) * H + h;
-    const float4 rec = ml[row];
+  for (int s0 = 0; s0 < S; s0 += 64) {
+    const float4 rec = s0 == 0 ? rec0 : record(s0);
     const float wgt = rec.x == -INFINITY ? 0.f : exp2f(rec.x - mx);
     l += wgt * rec.y;
     le += wgt * rec.z;
-    const float4* src = reinterpret_cast<const float4*>(ws_o + row * DV) + 2 * lane;
-    const float4 v0 = src[0], v1 = src[1];
-    o0.x += wgt * v0.x; o0.y += wgt * v0.y; o0.z += wgt * v0.z; o0.w += wgt * v0.w;
-    o1.x += wgt * v1.x; o1.y += wgt * v1.y; o1.z += wgt * v1.z; o1.w += wgt * v1.w;
+    const int n = min(64, S - s0);
+    for (int j0 = 0; j0 < n; j0 += COMBINE_BATCH) {
+      float4 v[COMBINE_BATCH][2];
+#pragma unroll
+      for (int j = 0; j < COMBINE_BATCH; ++j) {
+        const int jj = min(j0 + j, n - 1);
+        const float4* src =
+            reinterpret_cast<const float4*>(ws_o + ((size_t)(base + s0 + jj) * H + h) * DV) + 2 * lane;
+        v[j][0] = src[0];
+        v[j][1] = src[1];
+      }
+#pragma unroll
+      for (int j = 0; j < COMBINE_BATCH; ++j) {
+        if (j0 + j >= n) break;
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j0 + j));
+        o0.x += w * v[j][0].x; o0.y += w * v[j][0].y; o0.z += w * v[j][0].z; o0.w += w * v[j][0].w;
+        o1.x += w * v[j][1].x; o1.y += w * v[j][1].y; o1.z += w * v[j][1].z; o1.w += w * v[j][1].w;
+      }
+    }
   }
+  l = wave_sum(l);
+  le = wave_sum(le);
   const float inv = l > 0.f ? 1.f / l : 0.f;
   u32x4_t o;
   o[0] = to_q16<QT>(o0.x * inv) | (to_q16<QT>(o0.y * inv) << 16);
@@ -469,27 +507,6 @@ __device__ __forceinline__ void combine_head(int t, int h, int H, int S, int bas
   o[3] = to_q16<QT>(o1.z * inv) | (to_q16<QT>(o1.w * inv) << 16);
   reinterpret_cast<u32x4_t*>(out + ((size_t)t * H + h) * DV)[lane] = o;
   if (lse && lane == 0) lse[(size_t)t * H + h] = (mx + __log2f(le)) * 0.6931471805599453f;
-}
-
-// Called by every thread of a workgroup that has written split `split` of token t
-// (S splits, partial slots base ..): the partial is published (agent-scope
-// release), counted, and the workgroup that counts the last one merges all of
-// them (acquire) and resets the counter for the next call.  s_last is an LDS int.
-template <int QT>
-__device__ __forceinline__ void split_finish(int t, int H, int S, int base,
-                                             int* __restrict__ split_cnt, int& s_last,
-                                             const float* __restrict__ ws_o,
-                                             const float* __restrict__ ws_ml,
-                                             uint16_t* __restrict__ out, float* __restrict__ lse) {
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(&split_cnt[t], 1) == S - 1;
-  __syncthreads();
-  if (!s_last) return;
-  if (threadIdx.x == 0) split_cnt[t] = 0;
-  __threadfence();
-  const int nw = blockDim.x >> 6;
-  for (int h = threadIdx.x >> 6; h < H; h += nw) combine_head<QT>(t, h, H, S, base, ws_o, ws_ml, out, lse);
 }
 
 // OCP FP8 E4M3FN code -> exact 16-bit value of the query dtype.
@@ -528,7 +545,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
     const int* __restrict__ cmp_bt, const int* __restrict__ rows_list,
     const int* __restrict__ ncmp, const float* __restrict__ sinks, const int* __restrict__ plan,
     uint16_t* __restrict__ out, float* __restrict__ lse, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, int* __restrict__ split_cnt) {
+    float* __restrict__ ws_ml) {
   constexpr int DV = 512;
   constexpr int NT = 256;
   constexpr int ROWB = DQK * 2;          // LDS row bytes (16-bit elements)
@@ -545,7 +562,6 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
   __shared__ __attribute__((aligned(16))) uint8_t tiles[NBUF * TILEB];
   __shared__ const uint8_t* rowaddr[2][SAS_TILE];
   __shared__ float rowscale[SAS_TILE];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -568,7 +584,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
   }
 
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
-  const int b = tk[TK_B], nwin = tk[TK_NWIN];
+  const int nwin = tk[TK_NWIN];
   const int splits = tk[TK_SPLITS], wsbase = tk[TK_WSBASE];
   const int r0 = ur[1];
   const int r1 = min(ur[2], nwin + ncmp[t]);
@@ -792,8 +808,8 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
   }
 
   // ---- epilogue ----
+  if (!hvalid) return;
   if (splits == 1) {
-    if (!hvalid) return;
     const float inv = 1.f / l_run;
     uint16_t* orow = out + ((size_t)t * H + h) * DV;
 #pragma unroll
@@ -815,7 +831,6 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
     float* orow = ws_o + ((size_t)slot * H + h) * DV;
 #pragma unroll
     for (int mm = 0; mm < 8; ++mm) {
-      if (!hvalid) break;
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         float4 v0, v1;
@@ -832,33 +847,27 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(
         dst[1] = v1;
       }
     }
-    if (hvalid && g == 0)
+    if (g == 0)
       reinterpret_cast<float4*>(ws_ml)[(size_t)slot * H + h] = make_float4(m_run, l_run, l_run, 0.f);
-    // the last split of the token to finish merges the partials
-    split_finish<QT>(t, H, splits, wsbase, split_cnt, s_last, ws_o, ws_ml, out, lse);
   }
 }
 
 // ===========================================================================
-// Split combine as a pass of its own (sas_combine): one wave per (split token,
-// head), grid-stride over the split tokens the plan recorded.  The forward pass
-// merges in the last split unit of each token (split_finish); this pass rewrites
-// the same outputs from the partials the last attention pass left.
+// Split combine: one wave per (split token, head), grid-stride over the split
+// tokens the plan recorded (a call without split tokens exits at once).
 // ===========================================================================
-constexpr int COMBINE_HEADS = 4;  // waves (heads) per workgroup
+constexpr int COMBINE_WAVES = 4;  // waves per workgroup
 
 template <int QT>
-__global__ __launch_bounds__(64 * COMBINE_HEADS) void combine_kernel(
+__global__ __launch_bounds__(64 * COMBINE_WAVES) void combine_kernel(
     SasFwdArgs a, const int* __restrict__ plan, const float* __restrict__ ws_o,
     const float* __restrict__ ws_ml, uint16_t* __restrict__ out, float* __restrict__ lse) {
   const int H = a.H;
-  const int groups = (H + COMBINE_HEADS - 1) / COMBINE_HEADS;
-  const int items = plan[PH_NSPLIT_TOKENS] * groups;  // (split token, head group) pairs
+  const int items = plan[PH_NSPLIT_TOKENS] * H;  // (split token, head) pairs
   const SasPlanLayout L = sas_plan_layout(a.T, a.split_cap);
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
-    const int i = item / groups;
-    const int h = (item - i * groups) * COMBINE_HEADS + (threadIdx.x >> 6);
-    if (h >= H) continue;
+  const int wave = blockIdx.x * COMBINE_WAVES + (threadIdx.x >> 6);
+  for (int item = wave; item < items; item += gridDim.x * COMBINE_WAVES) {
+    const int i = item / H, h = item - i * H;
     const int t = plan[L.off_split_tokens + i];
     const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
     combine_head<QT>(t, h, H, tk[TK_SPLITS], tk[TK_WSBASE], ws_o, ws_ml, out, lse);

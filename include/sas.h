@@ -123,15 +123,14 @@ int sas_target_units(const sas_params_t* p, int32_t* units);
  * from q_prefix / act_q_lens / seqused_kv only (device pointers). */
 int sas_plan(const sas_params_t* p, const int32_t* q_prefix, const int32_t* act_q_lens,
              const int32_t* seqused_kv, int32_t* plan, size_t plan_n_int32, sas_stream_t stream);
-/* Full forward: (plan if plan == NULL) -> index resolution -> attention, where
- * the last split unit of each split token merges its partials.  plan may be a
- * buffer filled by sas_plan for the same params and lengths. */
+/* Full forward: (plan if plan == NULL) -> index resolution -> attention ->
+ * split combine.  plan may be a buffer filled by sas_plan for the same params
+ * and lengths. */
 int sas_forward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
                 void* workspace, size_t workspace_bytes, sas_stream_t stream);
 /* The stages of sas_forward, for timing and debugging (same workspace).
- * sas_attend writes the final output of every token (merging split tokens);
- * sas_combine re-merges the split partials of the last sas_attend into out/lse
- * as a pass of its own (same result). */
+ * sas_attend writes the output of every unsplit token and the partials of split
+ * tokens; sas_combine merges those partials into out / lse. */
 int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
                 void* workspace, size_t workspace_bytes, sas_stream_t stream);
 int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
