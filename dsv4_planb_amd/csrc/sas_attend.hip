@@ -1,4 +1,4 @@
-// sas_attend.hip -- pipelined gfx950 attention kernel for 16-bit (bf16 / fp16) KV.
+// sas_attend.hip -- pipelined gfx950 attention kernel for bf16 / fp16 and fp8 e4m3 KV.
 //
 // One workgroup (4 waves, one per SIMD) processes one work unit of the split-KV
 // plan: a contiguous range of one query token's row list (its window rows, then
@@ -53,6 +53,22 @@
 // 256 B, and the per-lane read offsets reduce to two registers plus immediates.
 // A latent DMA instruction copies one whole row (64 lanes x 16 B), so its source
 // is a wave-uniform row base plus a per-lane offset.
+//
+// fp8 e4m3 KV (KV8; each row 576 B of codes plus an fp32 scale): the tile holds the
+// codes and every MFMA operand is converted in registers (v_cvt_scalef32_pk_bf16_fp8,
+// exact: every e4m3 value is a bf16 / fp16 value).  Row r sits at 1056 r; its 16-B
+// chunk c at c ^ (9 ((r >> 3) & 1)).  One DMA instruction per row (64 lanes x 16 B:
+// lanes past the 36 chunks read out of range and write zeros into the row's
+// padding).  K fragments come from ds_read_b128 (two k-steps each; the Q fragments
+// follow the same dimension order); V^T fragments from ds_read_b64_tr_b8, whose
+// lane i of each 16-lane block receives byte i & 7 of lanes 2 p + (i >> 3), p = 0..7:
+// 8 keys of one dimension, one MFMA operand after four conversions.  With this
+// layout the b128 K reads (16 rows, one chunk) and the transposed V reads (8 rows x
+// 32 B per 32 lanes) touch every bank once per 256 B.  The scale multiplies S
+// (x = S c s) and is folded into P before its rounding (O = sum bf16(P s) V8, the
+// reference's dequantised V = V8 s).  The output normaliser sums the weights that
+// entered PV, bf16(P s) / s, so that O / l_w stays a convex combination of the rows
+// s V8 (a one-hot softmax returns s V8 exactly); l_e sums the unrounded P (LSE).
 #include <hip/hip_runtime.h>
 
 #include "sas_common.h"
@@ -62,6 +78,8 @@ namespace sas {
 constexpr float REDO_SLACK = 64.f;
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // Workgroup barrier without the memory fences of __syncthreads(): those wait for
 // every outstanding global load (vmcnt(0)), which would drain the DMA prefetch.
@@ -80,26 +98,52 @@ __device__ __forceinline__ int swz_a(int r) { return (r >> 2) & 3; }
 // Swizzle of the rope region.
 __device__ __forceinline__ int swz_b(int r) { return (r >> 1) & 7; }
 
-template <int DQK>
+// fp8 tiles: 32 rows at a 1056-B stride, then one 512-B scale block per wave: its 8
+// rows' scales s (then zeros) and, 256 B on, their 1 / s.
+constexpr int KV8_STRIDE = 1056;
+constexpr int KV8_SCALES = SAS_TILE * KV8_STRIDE;
+
+template <int DQK, bool KV8>
 struct AttendLds {
-  static constexpr int TILEB = SAS_TILE * (1024 + 64) + SAS_TILE * (DQK - 512) * 2;
+  static constexpr int TILEB =
+      KV8 ? KV8_SCALES + 4 * 512 : SAS_TILE * (1024 + 64) + SAS_TILE * (DQK - 512) * 2;
   uint8_t tiles[4 * TILEB];
   int far;  // a logit of some head outgrew the frame
 };
 
+// Two e4m3 codes (the low or the high half of a dword) -> two 16-bit values of the
+// query dtype, exactly.
+template <int QT, bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_q16(uint32_t v) {
+  if constexpr (QT == 0)
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v, 1.0f, HI));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v, 1.0f, HI));
+}
+
 // d = a b^T + 0 / d += a b^T in VGPRs (the O accumulator owns the AGPRs).  Written as
 // inline assembly so the S accumulator is a VGPR tuple; the chain's only hazard, a
 // VALU read of d, is covered by vgpr_mfma_drain.
-template <int QT>
+// CVT: the A operand was just written by VALU conversions, which an MFMA may read
+// only two wait states later (s_nop 1).
+template <int QT, bool CVT = false>
 __device__ __forceinline__ void vmfma_first(f32x16_t& d, const u32x4_t& a, const u32x4_t& b) {
-  if constexpr (QT == 0)
+  if constexpr (CVT && QT == 0)
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  else if constexpr (CVT)
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  else if constexpr (QT == 0)
     asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
   else
     asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
 }
-template <int QT>
+template <int QT, bool CVT = false>
 __device__ __forceinline__ void vmfma_acc(f32x16_t& d, const u32x4_t& a, const u32x4_t& b) {
-  if constexpr (QT == 0)
+  if constexpr (CVT && QT == 0)
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  else if constexpr (CVT)
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+  else if constexpr (QT == 0)
     asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
   else
     asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
@@ -132,10 +176,11 @@ __device__ __forceinline__ void wait_barrier() {
 template <bool STREAM>
 constexpr int gather_cpol() { return STREAM ? 2 : 0; }  // 2: the NT bit of the buffer load
 
-template <int DQK, int QT, bool STREAM, bool REDO>
+template <int DQK, int QT, bool STREAM, bool KV8, bool REDO>
 __device__ __forceinline__ bool attend_unit(
-    int u, AttendLds<DQK>& sm, const SasFwdArgs& a, const uint16_t* __restrict__ q,
-    const uint64_t* __restrict__ addr_list, const int* __restrict__ ncmp,
+    int u, AttendLds<DQK, KV8>& sm, const SasFwdArgs& a, const uint16_t* __restrict__ q,
+    const uint64_t* __restrict__ addr_list, const float* __restrict__ scale_list,
+    const int* __restrict__ ncmp,
     const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
     float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml, float& m_obs) {
   constexpr int DV = 512;
@@ -148,11 +193,13 @@ __device__ __forceinline__ bool attend_unit(
   constexpr int STRA = ROWA + 64;         // latent LDS row stride
   constexpr int ROWR = (DQK - DV) * 2;    // rope bytes per row (128 or 0)
   constexpr int TILEA = TILE * STRA;
-  constexpr int TILEB = TILEA + TILE * ROWR;
+  constexpr int TILEB = KV8 ? KV8_SCALES + 4 * 512 : TILEA + TILE * ROWR;
   constexpr int KSTEPS = DQK / 16;        // MFMA k-steps of Q K^T: 36 / 32
-  constexpr int CPT = 8 + (ROPE ? 8 : 0); // DMA instructions per wave per tile
+  // DMA instructions per wave per tile: 8 latent rows (+ 8 rope rows), or 8 fp8
+  // rows and their scales and inverse scales
+  constexpr int CPT = KV8 ? 10 : 8 + (ROPE ? 8 : 0);
   static_assert(TILE == 32, "the MFMA tiling assumes 32-key tiles");
-  static_assert(AttendLds<DQK>::TILEB == TILEB, "LDS layout");
+  static_assert(AttendLds<DQK, KV8>::TILEB == TILEB, "LDS layout");
   lds_u8* const tiles = (lds_u8*)sm.tiles;
 
   const int tid = threadIdx.x;
@@ -181,13 +228,24 @@ __device__ __forceinline__ bool attend_unit(
   const int ntiles = r1 > r0 ? (r1 - r0 + TILE - 1) / TILE : 0;
   // row addresses of this unit's list (pool addresses; -1 codes read the zero row)
   const uint64_t* alist = addr_list + (size_t)t * a.list_stride + r0;
+  // fp8: this unit's row scales; their inverses follow the whole scale list
+  const float* slist = KV8 ? scale_list + (size_t)t * a.list_stride + r0 : nullptr;
+  const size_t inv_off = (size_t)a.T * a.list_stride;
 
   // ---- per-lane LDS offsets (bytes within a tile) ----
   // K, latent k-step ks < 32: row li, chunk 2 ks + g -> kofs[ks & 1] + 64 (ks >> 1).
   // K, rope k-step 32 + j: row li, rope chunk 2 j + g -> kofs_r ^ 32 j (the row
   // offset TILEA + 128 li has clear bits 4..6, which carry the swizzled chunk).
-  uint32_t kofs[2], kofs_r;
-  {
+  // fp8: K k-steps 2 j, 2 j + 1 come from one b128 read of row li, chunk 2 j + g at
+  // position (2 j + g) ^ 9 b3 (b3 = (li >> 3) & 1): byte 32 (j ^ 4 b3) + 16 (g ^ b3),
+  // i.e. kofs[(j >> 2) & 1] + 32 (j & ~4).
+  uint32_t kofs[2], kofs_r = 0;
+  if constexpr (KV8) {
+    const uint32_t b3 = (li >> 3) & 1;
+    const uint32_t base = li * KV8_STRIDE + 16 * (g ^ b3);
+    kofs[0] = base + 128 * b3;
+    kofs[1] = base + 128 * (1 - b3);
+  } else {
     const int f = swz_a(li);
 #pragma unroll
     for (int j = 0; j < 2; ++j) kofs[j] = li * STRA + 16 * ((2 * j + g) ^ f);
@@ -202,8 +260,21 @@ __device__ __forceinline__ bool attend_unit(
   // 4 mb + clo, clo = 2 (l & 1) + ((l >> 4) & 1), byte 8 ((l >> 1) & 1) within it.  The
   // row's swizzle only touches clo and depends on hf alone, so the offset is
   // vofs[hf] + 64 mb + 16 kk STRA.
+  // fp8 (ds_read_b64_tr_b8): MFMA row m of d-block mb is d = 32 mb + m.  Lane s of
+  // 16-lane block blk (p = (s & 15) >> 1, g = blk >> 1) supplies the row of the key
+  // that P^T's k index 8 g + p holds, 16 kk + 8 (p >> 2) + 4 g + (p & 3), at
+  // dimensions 32 mb + 16 (blk & 1) + 8 (s & 1) .. + 7: chunk 2 mb + (blk & 1) at
+  // position 2 (mb ^ 4 b3) + ((blk & 1) ^ b3), b3 = p >> 2, i.e.
+  // vofs[(mb >> 2) & 1] + 32 (mb & ~4) + 16 kk KV8_STRIDE.
   uint32_t vofs[2];
-  {
+  if constexpr (KV8) {
+    const int blk = lane >> 4, p = (lane & 15) >> 1;
+    const uint32_t b3 = p >> 2;
+    const int row = 8 * (p >> 2) + 4 * (blk >> 1) + (p & 3);
+    const uint32_t base = row * KV8_STRIDE + 16 * ((blk & 1) ^ b3) + 8 * (lane & 1);
+    vofs[0] = base + 128 * b3;
+    vofs[1] = base + 128 * (1 - b3);
+  } else {
     const int clo = 2 * (lane & 1) + ((lane >> 4) & 1);
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
@@ -251,8 +322,10 @@ __device__ __forceinline__ bool attend_unit(
   u32x4_t qf[KSTEPS];
   {
     const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(q + ((size_t)t * H + hc) * DQK);
+    // fp8: k-step 2 j + h covers dimensions 32 j + 16 g + 8 h .. + 7 (the K order)
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = qrow[2 * ks + g];
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qf[ks] = KV8 ? qrow[4 * (ks >> 1) + 2 * g + (ks & 1)] : qrow[2 * ks + g];
   }
   f32x16_t acc[16];
 #pragma unroll
@@ -266,7 +339,10 @@ __device__ __forceinline__ bool attend_unit(
   // loads an iteration before their DMA.
   const int wu = __builtin_amdgcn_readfirstlane(w);  // the wave index as a scalar
   const uint32_t ulane = (uint32_t)lane;
-  const uint32_t voffA0 = 16u * (ulane ^ (uint32_t)((2 * wu) & 3));
+  // fp8: every row of wave w has bit 3 of its tile row equal to w & 1, so lane l
+  // fetches chunk l ^ 9 (w & 1) of each of its rows (chunks past the row: zeros).
+  const uint32_t voffA0 = KV8 ? 16u * (ulane ^ (9u * (uint32_t)(wu & 1)))
+                              : 16u * (ulane ^ (uint32_t)((2 * wu) & 3));
   const uint32_t voffA1 = 16u * (ulane ^ (uint32_t)((2 * wu + 1) & 3));
   // rope DMA of row 8 w + k: lane l fetches chunk l ^ ((4 w + (k >> 1)) & 7)
   const uint32_t voffR0 = 16u * (ulane & 7u);
@@ -288,12 +364,31 @@ __device__ __forceinline__ bool attend_unit(
   // LDS, never the FLAT form: an outstanding FLAT load that writes LDS makes every
   // later LDS wait a full drain).
   auto row_rsrc = [&](uint64_t addr) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)addr, (short)0, ROWA + ROWR, 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)addr, (short)0, KV8 ? DQK : ROWA + ROWR,
+                                             0x00020000);
   };
+  // 16-bit KV: the latent 1024 B of row 8 w + k; fp8: the whole row
   auto dma_lat = [&](int i, const RowAddrs& ra, int k) {
-    lds_u8* dst = tiles + (i & (NSTAGE - 1)) * TILEB + (8 * wu + k) * STRA;
+    lds_u8* dst = tiles + (i & (NSTAGE - 1)) * TILEB + (8 * wu + k) * (KV8 ? KV8_STRIDE : STRA);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(row_rsrc(ra[k]), (void __attribute__((address_space(3)))*)dst, 16,
-                                             k < 4 ? voffA0 : voffA1, 0, 0, gather_cpol<STREAM>());
+                                             KV8 || k < 4 ? voffA0 : voffA1, 0, 0, gather_cpol<STREAM>());
+  };
+  // fp8: the scales of this wave's 8 rows of tile i into its block, then their
+  // inverses 256 B on (lane l writes float l; rows past the unit's end, and lanes
+  // 8 .. 63, read as zeros)
+  auto dma_scale = [&](int i) {
+    // (readfirstlane: a clamp selects v_med3, and a buffer resource in VGPRs would
+    // be issued lane by lane)
+    const int n = __builtin_amdgcn_readfirstlane(max(0, min(8, r1 - (r0 + i * TILE + 8 * wu))));
+    lds_u8* dst = tiles + (i & (NSTAGE - 1)) * TILEB + KV8_SCALES + 512 * wu;
+    const float* src = slist + i * TILE + 8 * wu;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, 4 * n, 0x00020000),
+        (void __attribute__((address_space(3)))*)dst, 4, 4u * ulane, 0, 0, gather_cpol<STREAM>());
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        __builtin_amdgcn_make_buffer_rsrc((void*)(src + inv_off), (short)0, 4 * n, 0x00020000),
+        (void __attribute__((address_space(3)))*)(dst + 256), 4, 4u * ulane, 0, 0,
+        gather_cpol<STREAM>());
   };
   // Rope: lanes 0..7 copy the 128-B rope of one row per instruction, chunk
   // l ^ swz_b(8 w + k) = l ^ ((4 w + (k >> 1)) & 7) into slot l.  It runs after every
@@ -324,7 +419,36 @@ __device__ __forceinline__ bool attend_unit(
     return ks < 32 ? lds_read_b128(tl + kofs[ks & 1] + 64 * (ks >> 1))
                    : lds_read_b128(tl + (kr ^ (32u * (uint32_t)(ks - 32))));
   };
+  // fp8: b128 read j holds k-steps 2 j (dwords 0, 1) and 2 j + 1 (dwords 2, 3)
+  auto kpair8 = [&](const lds_u8* tl, int j) -> u32x4_t {
+    return lds_read_b128(tl + kofs[(j >> 2) & 1] + 32 * (j & ~4));
+  };
   auto qk = [&](const lds_u8* tl, f32x16_t& s, auto&& work) {
+    if constexpr (KV8) {
+      u32x4_t rw[2];
+      rw[0] = kpair8(tl, 0);
+      rw[1] = kpair8(tl, 1);
+      SB();
+      work(-1);
+      SB();
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const int j = ks >> 1, h2 = 2 * (ks & 1);
+        u32x4_t kf;
+        kf[0] = fp8x2_to_q16<QT, false>(rw[j & 1][h2]);
+        kf[1] = fp8x2_to_q16<QT, true>(rw[j & 1][h2]);
+        kf[2] = fp8x2_to_q16<QT, false>(rw[j & 1][h2 + 1]);
+        kf[3] = fp8x2_to_q16<QT, true>(rw[j & 1][h2 + 1]);
+        if (ks == 0)
+          vmfma_first<QT, true>(s, kf, qf[0]);
+        else
+          vmfma_acc<QT, true>(s, kf, qf[ks]);
+        if ((ks & 1) && j + 2 < KSTEPS / 2) rw[j & 1] = kpair8(tl, j + 2);
+        work(ks);
+        SB();
+      }
+      return;
+    }
     // the rope offset, formed per chain rather than kept across the loop
     uint32_t kr = kofs_r;
     asm volatile("" : "+v"(kr));
@@ -350,7 +474,12 @@ __device__ __forceinline__ bool attend_unit(
   // (behind a lane < 8 branch) after the last MFMA.
   auto dma_step = [&](int ks, int i, const RowAddrs& ra) {
     if (ks >= 0 && (ks & 3) == 1 && (ks >> 2) < 8) dma_lat(i, ra, ks >> 2);
-    if (ks == KSTEPS - 1) dma_rope(i, ra);
+    if (ks == KSTEPS - 1) {
+      if constexpr (KV8)
+        dma_scale(i);
+      else
+        dma_rope(i, ra);
+    }
   };
 
   // ---- O^T += V^T P^T ----
@@ -365,6 +494,61 @@ __device__ __forceinline__ bool attend_unit(
     const uint32_t a1 = (uint32_t)(uintptr_t)tl + vofs[1];
     typedef uint32_t u32x16_t __attribute__((ext_vector_type(16)));
     u32x16_t sa;
+    if constexpr (KV8) {
+      // fp8: V^T fragments by ds_read_b64_tr_b8 into a three-deep ring v[250:255],
+      // three MFMAs ahead; four conversions into v[242:245] / v[246:249] each, two
+      // wait states (s_nop 1, after the next read) before the MFMA reads them.
+#define PV8_ASM(MN, CVT) \
+    asm volatile( \
+        "s_load_dwordx16 %[sa], %[ap], 0x0\n\t" \
+        "ds_read_b64_tr_b8 v[250:251], %[a0] offset:0\n\t" "ds_read_b64_tr_b8 v[252:253], %[a0] offset:32\n\t" "ds_read_b64_tr_b8 v[254:255], %[a0] offset:64\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v250, 1.0\n\t" CVT " v243, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v251, 1.0\n\t" CVT " v245, v251, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[250:251], %[a0] offset:96\n\t" "s_nop 1\n\t" MN " %[c0], v[242:245], %[p0], %[c0]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v252, 1.0\n\t" CVT " v247, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v253, 1.0\n\t" CVT " v249, v253, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[252:253], %[a1] offset:0\n\t" "s_nop 1\n\t" MN " %[c1], v[246:249], %[p0], %[c1]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v254, 1.0\n\t" CVT " v243, v254, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v255, 1.0\n\t" CVT " v245, v255, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[254:255], %[a1] offset:32\n\t" "s_nop 1\n\t" MN " %[c2], v[242:245], %[p0], %[c2]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v250, 1.0\n\t" CVT " v247, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v251, 1.0\n\t" CVT " v249, v251, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[250:251], %[a1] offset:64\n\t" "s_nop 1\n\t" MN " %[c3], v[246:249], %[p0], %[c3]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v252, 1.0\n\t" CVT " v243, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v253, 1.0\n\t" CVT " v245, v253, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[252:253], %[a1] offset:96\n\t" "s_nop 1\n\t" MN " %[c4], v[242:245], %[p0], %[c4]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v254, 1.0\n\t" CVT " v247, v254, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v255, 1.0\n\t" CVT " v249, v255, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[254:255], %[a0] offset:256\n\t" "s_nop 1\n\t" MN " %[c5], v[246:249], %[p0], %[c5]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v250, 1.0\n\t" CVT " v243, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v251, 1.0\n\t" CVT " v245, v251, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[250:251], %[a0] offset:288\n\t" "s_nop 1\n\t" MN " %[c6], v[242:245], %[p0], %[c6]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v252, 1.0\n\t" CVT " v247, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v253, 1.0\n\t" CVT " v249, v253, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[252:253], %[a0] offset:320\n\t" "s_nop 1\n\t" MN " %[c7], v[246:249], %[p0], %[c7]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v254, 1.0\n\t" CVT " v243, v254, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v255, 1.0\n\t" CVT " v245, v255, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[254:255], %[a0] offset:352\n\t" "s_nop 1\n\t" MN " %[c8], v[242:245], %[p0], %[c8]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v250, 1.0\n\t" CVT " v247, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v251, 1.0\n\t" CVT " v249, v251, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[250:251], %[a1] offset:256\n\t" "s_nop 1\n\t" MN " %[c9], v[246:249], %[p0], %[c9]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v252, 1.0\n\t" CVT " v243, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v253, 1.0\n\t" CVT " v245, v253, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[252:253], %[a1] offset:288\n\t" "s_nop 1\n\t" MN " %[c10], v[242:245], %[p0], %[c10]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v254, 1.0\n\t" CVT " v247, v254, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v255, 1.0\n\t" CVT " v249, v255, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[254:255], %[a1] offset:320\n\t" "s_nop 1\n\t" MN " %[c11], v[246:249], %[p0], %[c11]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v250, 1.0\n\t" CVT " v243, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v251, 1.0\n\t" CVT " v245, v251, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[250:251], %[a1] offset:352\n\t" "s_nop 1\n\t" MN " %[c12], v[242:245], %[p0], %[c12]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v252, 1.0\n\t" CVT " v247, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v253, 1.0\n\t" CVT " v249, v253, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[252:253], %[a0] offset:16896\n\t" "s_nop 1\n\t" MN " %[c13], v[246:249], %[p0], %[c13]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v254, 1.0\n\t" CVT " v243, v254, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v255, 1.0\n\t" CVT " v245, v255, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[254:255], %[a0] offset:16928\n\t" "s_nop 1\n\t" MN " %[c14], v[242:245], %[p0], %[c14]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v250, 1.0\n\t" CVT " v247, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v251, 1.0\n\t" CVT " v249, v251, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[250:251], %[a0] offset:16960\n\t" "s_nop 1\n\t" MN " %[c15], v[246:249], %[p0], %[c15]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v252, 1.0\n\t" CVT " v243, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v253, 1.0\n\t" CVT " v245, v253, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[252:253], %[a0] offset:16992\n\t" "s_nop 1\n\t" MN " %[c0], v[242:245], %[p1], %[c0]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v254, 1.0\n\t" CVT " v247, v254, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v255, 1.0\n\t" CVT " v249, v255, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[254:255], %[a1] offset:16896\n\t" "s_nop 1\n\t" MN " %[c1], v[246:249], %[p1], %[c1]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v250, 1.0\n\t" CVT " v243, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v251, 1.0\n\t" CVT " v245, v251, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[250:251], %[a1] offset:16928\n\t" "s_nop 1\n\t" MN " %[c2], v[242:245], %[p1], %[c2]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v252, 1.0\n\t" CVT " v247, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v253, 1.0\n\t" CVT " v249, v253, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[252:253], %[a1] offset:16960\n\t" "s_nop 1\n\t" MN " %[c3], v[246:249], %[p1], %[c3]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v254, 1.0\n\t" CVT " v243, v254, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v255, 1.0\n\t" CVT " v245, v255, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[254:255], %[a1] offset:16992\n\t" "s_nop 1\n\t" MN " %[c4], v[242:245], %[p1], %[c4]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v250, 1.0\n\t" CVT " v247, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v251, 1.0\n\t" CVT " v249, v251, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[250:251], %[a0] offset:17152\n\t" "s_nop 1\n\t" MN " %[c5], v[246:249], %[p1], %[c5]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v252, 1.0\n\t" CVT " v243, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v253, 1.0\n\t" CVT " v245, v253, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[252:253], %[a0] offset:17184\n\t" "s_nop 1\n\t" MN " %[c6], v[242:245], %[p1], %[c6]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v254, 1.0\n\t" CVT " v247, v254, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v255, 1.0\n\t" CVT " v249, v255, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[254:255], %[a0] offset:17216\n\t" "s_nop 1\n\t" MN " %[c7], v[246:249], %[p1], %[c7]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v250, 1.0\n\t" CVT " v243, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v251, 1.0\n\t" CVT " v245, v251, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[250:251], %[a0] offset:17248\n\t" "s_nop 1\n\t" MN " %[c8], v[242:245], %[p1], %[c8]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v252, 1.0\n\t" CVT " v247, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v253, 1.0\n\t" CVT " v249, v253, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[252:253], %[a1] offset:17152\n\t" "s_nop 1\n\t" MN " %[c9], v[246:249], %[p1], %[c9]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v254, 1.0\n\t" CVT " v243, v254, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v255, 1.0\n\t" CVT " v245, v255, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[254:255], %[a1] offset:17184\n\t" "s_nop 1\n\t" MN " %[c10], v[242:245], %[p1], %[c10]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v250, 1.0\n\t" CVT " v247, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v251, 1.0\n\t" CVT " v249, v251, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[250:251], %[a1] offset:17216\n\t" "s_nop 1\n\t" MN " %[c11], v[246:249], %[p1], %[c11]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v242, v252, 1.0\n\t" CVT " v243, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v253, 1.0\n\t" CVT " v245, v253, 1.0 op_sel:[1,0,0]\n\t" "ds_read_b64_tr_b8 v[252:253], %[a1] offset:17248\n\t" "s_nop 1\n\t" MN " %[c12], v[242:245], %[p1], %[c12]\n\t" \
+        "s_waitcnt lgkmcnt(2)\n\t" CVT " v246, v254, 1.0\n\t" CVT " v247, v254, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v255, 1.0\n\t" CVT " v249, v255, 1.0 op_sel:[1,0,0]\n\t" "s_nop 1\n\t" MN " %[c13], v[246:249], %[p1], %[c13]\n\t" \
+        "s_waitcnt lgkmcnt(1)\n\t" CVT " v242, v250, 1.0\n\t" CVT " v243, v250, 1.0 op_sel:[1,0,0]\n\t" CVT " v244, v251, 1.0\n\t" CVT " v245, v251, 1.0 op_sel:[1,0,0]\n\t" "s_nop 1\n\t" MN " %[c14], v[242:245], %[p1], %[c14]\n\t" \
+        "s_waitcnt lgkmcnt(0)\n\t" CVT " v246, v252, 1.0\n\t" CVT " v247, v252, 1.0 op_sel:[1,0,0]\n\t" CVT " v248, v253, 1.0\n\t" CVT " v249, v253, 1.0 op_sel:[1,0,0]\n\t" "s_nop 1\n\t" MN " %[c15], v[246:249], %[p1], %[c15]\n\t" \
+        : [sa] "=s"(sa), [c0] "+a"(acc[0]), [c1] "+a"(acc[1]), [c2] "+a"(acc[2]), [c3] "+a"(acc[3]), \
+          [c4] "+a"(acc[4]), [c5] "+a"(acc[5]), [c6] "+a"(acc[6]), [c7] "+a"(acc[7]), \
+          [c8] "+a"(acc[8]), [c9] "+a"(acc[9]), [c10] "+a"(acc[10]), [c11] "+a"(acc[11]), \
+          [c12] "+a"(acc[12]), [c13] "+a"(acc[13]), [c14] "+a"(acc[14]), [c15] "+a"(acc[15]) \
+        : [a0] "v"(a0), [a1] "v"(a1), [p0] "v"(pk[0]), [p1] "v"(pk[1]), [ap] "s"(aptr) \
+        : "v242", "v243", "v244", "v245", "v246", "v247", "v248", "v249", "v250", "v251", \
+          "v252", "v253", "v254", "v255", "memory");
+      if constexpr (QT == 0) {
+        PV8_ASM("v_mfma_f32_32x32x16_bf16", "v_cvt_scalef32_pk_bf16_fp8")
+      } else {
+        PV8_ASM("v_mfma_f32_32x32x16_f16", "v_cvt_scalef32_pk_f16_fp8")
+      }
+#undef PV8_ASM
+      return __builtin_bit_cast(RowAddrs, sa);
+    }
 #define PV_RD(j, b) \
     "ds_read_b64_tr_b16 v[" #b ":" #b "+1], %[a0] offset:" #j "\n\t" \
     "ds_read_b64_tr_b16 v[" #b "+2:" #b "+3], %[a1] offset:" #j "\n\t"
@@ -447,13 +631,19 @@ __device__ __forceinline__ bool attend_unit(
   // Every phase ends by pinning what it wrote (an empty volatile asm that takes and
   // gives the values): volatile asm keeps its place among the MFMA statements, so
   // the optimiser can neither sink the work out of the chain nor merge phases.
-  auto sm_phase = [&](f32x16_t& x, u32x4_t(&pk)[2], int k, int ph, bool scaled) {
+  // fp8: sc holds the scales of rows 2 k, 2 k + 1 and iv their inverses (x = S c s;
+  // bf16(P s) enters PV and bf16(P s) / s the output normaliser).
+  auto sm_phase = [&](f32x16_t& x, u32x4_t(&pk)[2], int k, int ph, bool scaled, f32x2_t sc,
+                      f32x2_t iv) {
     const int r = 2 * k;
     float x0 = x[r], x1 = x[r + 1];
     if (ph == 0) {
       if (scaled) {
         x0 -= m_run;
         x1 -= m_run;
+      } else if constexpr (KV8) {
+        x0 = fmaf(x0, c * sc[0], -m_run);
+        x1 = fmaf(x1, c * sc[1], -m_run);
       } else {
         x0 = fmaf(x0, c, -m_run);
         x1 = fmaf(x1, c, -m_run);
@@ -466,11 +656,16 @@ __device__ __forceinline__ bool attend_unit(
       x1 = __builtin_amdgcn_exp2f(x1);
       asm volatile("" : "+v"(x0), "+v"(x1));
     } else if (ph == 2) {
-      uint32_t p = pack2_q16<QT>(x0, x1);
+      uint32_t p = KV8 ? pack2_q16<QT>(x0 * sc[0], x1 * sc[1]) : pack2_q16<QT>(x0, x1);
       float e = pe + (x0 + x1);
       asm volatile("" : "+v"(p), "+v"(e));
       pk[k >> 2][k & 3] = p;
       pe = e;
+    } else if constexpr (KV8) {
+      const uint32_t p = pk[k >> 2][k & 3];
+      float w2 = fmaf(q16_to_f32<QT>(p >> 16), iv[1], fmaf(q16_to_f32<QT>(p & 0xffffu), iv[0], pw));
+      asm volatile("" : "+v"(w2));
+      pw = w2;
     } else {
       float w2 = sum2_q16<QT>(pk[k >> 2][k & 3], pw);
       asm volatile("" : "+v"(w2));
@@ -484,10 +679,68 @@ __device__ __forceinline__ bool attend_unit(
   // 30).  First tile of the unit (the frame is not fixed yet): scale at steps -1
   // and 0, the tile max at step 1, then chunk k's phase p at step 3k + p + 2
   // (steps 2 .. 26).
+  // fp8 (tc: the tile being softmaxed, whose scale blocks hold its row scales):
+  //   steady: chunk k's phase p at step 4k + p + 1; its scales are read a chunk ahead
+  //   into sc8[k & 1] (chunk 0's at step -1), its inverse scales at its phase 1;
+  //   first tile: all 16 scales at step -1 (s16), x = S c s at steps 0 and 1, the tile
+  //   max at step 2, chunk k's phase p at step 3k + p + 3, its scales read again at
+  //   its phase 0 and its inverse scales at its phase 1.
+  // Register r of S^T is key 8 (r >> 2) + 4 g + (r & 3), whose scale is at byte
+  // 512 (r >> 2) + 16 g + 4 (r & 3) of the scale blocks and its inverse 256 B on.
+  auto scl2 = [&](const lds_u8* tl, int k, int inv) -> f32x2_t {
+    return *reinterpret_cast<const __attribute__((address_space(3))) f32x2_t*>(
+        tl + KV8_SCALES + 256 * inv + 512 * (k >> 1) + 16 * g + 8 * (k & 1));
+  };
+  auto scl4 = [&](const lds_u8* tl, int qd) -> f32x4_t {
+    return *reinterpret_cast<const __attribute__((address_space(3))) f32x4_t*>(
+        tl + KV8_SCALES + 512 * qd + 16 * g);
+  };
+  auto s16_pair = [](const f32x4_t (&s16)[4], int k) -> f32x2_t {
+    const f32x4_t v = s16[k >> 1];
+    return (k & 1) ? f32x2_t{v[2], v[3]} : f32x2_t{v[0], v[1]};
+  };
+  auto s16_at = [](const f32x4_t (&s16)[4], int r) -> float { return s16[r >> 2][r & 3]; };
+  auto sm_step8 = [&](f32x16_t& x, u32x4_t(&pk)[2], int ks, bool first, const lds_u8* tc,
+                      f32x2_t (&sc8)[2], f32x2_t& iv8, f32x4_t (&s16)[4]) {
+    if (!first) {
+      if (ks == -1) sc8[0] = scl2(tc, 0, 0);
+      const int k = (ks - 1) >> 2, ph = (ks - 1) & 3;
+      if (ks >= 1 && k < 8) {
+        if (ph == 0 && k + 1 < 8) sc8[(k + 1) & 1] = scl2(tc, k + 1, 0);
+        if (ph == 1) iv8 = scl2(tc, k, 1);
+        sm_phase(x, pk, k, ph, false, sc8[k & 1], iv8);
+      }
+    } else if (ks == -1) {
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) s16[qd] = scl4(tc, qd);
+    } else if (ks == 0 || ks == 1) {
+#pragma unroll
+      for (int r = 0; r < 8; r += 2) {
+        const int rr = 8 * ks + r;
+        float x0 = x[rr] * (c * s16_at(s16, rr)), x1 = x[rr + 1] * (c * s16_at(s16, rr + 1));
+        asm volatile("" : "+v"(x0), "+v"(x1));
+        x[rr] = x0;
+        x[rr + 1] = x1;
+      }
+    } else if (ks == 2) {
+      float m = fmaxf(m_run, tile_max(x));
+      asm volatile("" : "+v"(m));
+      m_run = m;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int ph = ks - 3 - 3 * k;
+        if (ph == 0) sc8[k & 1] = scl2(tc, k, 0);
+        if (ph == 1) iv8 = scl2(tc, k, 1);
+        if (ph >= 0 && ph < 4) sm_phase(x, pk, k, ph, true, sc8[k & 1], iv8);
+      }
+    }
+  };
   auto sm_step = [&](f32x16_t& x, u32x4_t(&pk)[2], int ks, bool first) {
+    const f32x2_t none = {1.f, 1.f};
     if (!first) {
       const int k = (ks + 1) >> 2, ph = (ks + 1) & 3;
-      if (ks >= -1 && k < 8) sm_phase(x, pk, k, ph, false);
+      if (ks >= -1 && k < 8) sm_phase(x, pk, k, ph, false, none, none);
     } else if (ks == -1 || ks == 0) {
 #pragma unroll
       for (int r = 0; r < 8; r += 2) {
@@ -504,14 +757,22 @@ __device__ __forceinline__ bool attend_unit(
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int ph = ks - 2 - 3 * k;
-        if (ph >= 0 && ph < 4) sm_phase(x, pk, k, ph, true);
+        if (ph >= 0 && ph < 4) sm_phase(x, pk, k, ph, true, none, none);
       }
     }
   };
   // The unit's last tile, on its own (rows past r1 masked).
-  auto softmax_last = [&](f32x16_t& x, u32x4_t(&pk)[2], bool first, int nvalid) {
+  auto softmax_last = [&](f32x16_t& x, u32x4_t(&pk)[2], bool first, int nvalid, const lds_u8* tc) {
+    f32x4_t s16[4];
+    if constexpr (KV8) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] *= c;
+      for (int qd = 0; qd < 4; ++qd) s16[qd] = scl4(tc, qd);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] *= c * s16_at(s16, r);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] *= c;
+    }
     if (nvalid < TILE) {
       const int lim = nvalid - 4 * g;
 #pragma unroll
@@ -520,9 +781,12 @@ __device__ __forceinline__ bool attend_unit(
     }
     if (first) m_run = fmaxf(m_run, tile_max(x));
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < 8; ++k) {
+      const f32x2_t iv = KV8 ? scl2(tc, k, 1) : f32x2_t{1.f, 1.f};
 #pragma unroll
-      for (int ph = 0; ph < 4; ++ph) sm_phase(x, pk, k, ph, true);
+      for (int ph = 0; ph < 4; ++ph)
+        sm_phase(x, pk, k, ph, true, KV8 ? s16_pair(s16, k) : f32x2_t{1.f, 1.f}, iv);
+    }
   };
 
   if (!REDO && tid == 0) sm.far = 0;
@@ -533,18 +797,17 @@ __device__ __forceinline__ bool attend_unit(
     // O += V(i)^T P(i)^T.  Tiles i, i+1 and i+3 sit in distinct slots; tiles
     // i+2 and i+3 are in flight while i+1 is computed.  Tiles past the last one
     // are DMA'd from the zero row, so every wait counts the same instructions.
-    RowAddrs ra_next = load_addrs(0);
+    RowAddrs ra_next;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) dma_lat(0, ra_next, k);
-    dma_rope(0, ra_next);
-    ra_next = load_addrs(1);
+    for (int i0 = 0; i0 < 3; ++i0) {
+      ra_next = load_addrs(i0);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) dma_lat(1, ra_next, k);
-    dma_rope(1, ra_next);
-    ra_next = load_addrs(2);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) dma_lat(2, ra_next, k);
-    dma_rope(2, ra_next);
+      for (int k = 0; k < 8; ++k) dma_lat(i0, ra_next, k);
+      if constexpr (KV8)
+        dma_scale(i0);
+      else
+        dma_rope(i0, ra_next);
+    }
     ra_next = load_addrs(3);
 
     f32x16_t s_cur, s_next;
@@ -564,19 +827,29 @@ __device__ __forceinline__ bool attend_unit(
         wait_barrier();
         const RowAddrs ra_cur = ra_next;
         const lds_u8* tn = tiles + ((i + 1) & (NSTAGE - 1)) * TILEB;
+        const lds_u8* tc = tiles + (i & (NSTAGE - 1)) * TILEB;  // tile i (its scales)
+        f32x2_t sc8[2], iv8;
+        f32x4_t s16[4];
         if (!REDO && i == 0) {
           qk(tn, s_next, [&](int ks) {
-            sm_step(s_cur, pk, ks, true);
+            if constexpr (KV8)
+              sm_step8(s_cur, pk, ks, true, tc, sc8, iv8, s16);
+            else
+              sm_step(s_cur, pk, ks, true);
             dma_step(ks, i + 3, ra_cur);
           });
         } else {
           qk(tn, s_next, [&](int ks) {
-            sm_step(s_cur, pk, ks, false);
+            if constexpr (KV8)
+              sm_step8(s_cur, pk, ks, false, tc, sc8, iv8, s16);
+            else
+              sm_step(s_cur, pk, ks, false);
             dma_step(ks, i + 3, ra_cur);
           });
         }
       } else {
-        softmax_last(s_cur, pk, !REDO && i == 0, r1 - (r0 + i * TILE));
+        softmax_last(s_cur, pk, !REDO && i == 0, r1 - (r0 + i * TILE),
+                     tiles + (i & (NSTAGE - 1)) * TILEB);
       }
       SB();
       // PV of tile i, carrying the scalar load of tile i+4's row addresses (after
@@ -626,6 +899,23 @@ __device__ __forceinline__ bool attend_unit(
   if (!hvalid) return false;
   if (splits == 1) {
     const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
+    if constexpr (KV8) {  // register 4 q + e of block mb: d = 32 mb + 8 q + 4 g + e
+      uint16_t* orow = out + ((size_t)t * H + h) * DV + 4 * g;
+#pragma unroll
+      for (int mb = 0; mb < 16; ++mb) {
+        f32x16_t v = acc[mb];
+        asm volatile("" : "+v"(v));
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          uint2 o;
+          o.x = pack2_q16<QT>(v[4 * qd] * inv, v[4 * qd + 1] * inv);
+          o.y = pack2_q16<QT>(v[4 * qd + 2] * inv, v[4 * qd + 3] * inv);
+          *reinterpret_cast<uint2*>(orow + 32 * mb + 8 * qd) = o;
+        }
+      }
+      if (lse && g == 0) lse[(size_t)t * H + h] = (m_run + __log2f(l_e)) * 0.6931471805599453f;
+      return false;
+    }
     uint16_t* orow = out + ((size_t)t * H + h) * DV + 16 * g;
     // One 16-register block at a time into VGPRs (the pin keeps the copies in
     // step with the stores: copied all at once, the 256 accumulators overflow
@@ -646,7 +936,9 @@ __device__ __forceinline__ bool attend_unit(
     if (lse && g == 0) lse[(size_t)t * H + h] = (m_run + __log2f(l_e)) * 0.6931471805599453f;
   } else {  // an un-normalised partial (O, m, l_w, l_e) for the combine pass
     const int slot = wsbase + split;
-    float* orow = ws_o + ((size_t)slot * H + h) * DV + 16 * g;
+    // registers 4 qd .. 4 qd + 3 of block mb: d = 32 mb + 16 g + 4 qd .. (16-bit KV),
+    // 32 mb + 8 qd + 4 g .. (fp8)
+    float* orow = ws_o + ((size_t)slot * H + h) * DV + (KV8 ? 4 : 16) * g;
 #pragma unroll
     for (int mb = 0; mb < 16; ++mb) {
 #pragma unroll
@@ -656,7 +948,7 @@ __device__ __forceinline__ bool attend_unit(
         v.y = acc[mb][4 * qd + 1];
         v.z = acc[mb][4 * qd + 2];
         v.w = acc[mb][4 * qd + 3];
-        *reinterpret_cast<float4*>(orow + 32 * mb + 4 * qd) = v;
+        *reinterpret_cast<float4*>(orow + 32 * mb + (KV8 ? 8 : 4) * qd) = v;
       }
     }
     if (g == 0)
@@ -670,22 +962,21 @@ __device__ __forceinline__ bool attend_unit(
 namespace sas {
 
 // One workgroup per work unit.
-template <int DQK, int QT, bool STREAM>
+template <int DQK, int QT, bool STREAM, bool KV8>
 __global__ __launch_bounds__(256, 1) void attend_kernel(
-    SasFwdArgs a, const uint16_t* __restrict__ q, const uint8_t* __restrict__ ori_kv,
-    const uint8_t* __restrict__ cmp_kv, const int* __restrict__ cmp_bt,
-    const uint64_t* __restrict__ addr_list, const int* __restrict__ ncmp,
+    SasFwdArgs a, const uint16_t* __restrict__ q, const uint64_t* __restrict__ addr_list,
+    const float* __restrict__ scale_list, const int* __restrict__ ncmp,
     const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
     float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
-  __shared__ __attribute__((aligned(16))) AttendLds<DQK> sm;
+  __shared__ __attribute__((aligned(16))) AttendLds<DQK, KV8> sm;
   const int u = blockIdx.x;
   if (plan[PH_MAGIC] != SAS_PLAN_MAGIC || u >= plan[PH_UNITS]) return;
   float m_obs = 0.f;
-  if (attend_unit<DQK, QT, STREAM, false>(u, sm, a, q, addr_list, ncmp, sinks, plan, out, lse, ws_o,
-                                          ws_ml, m_obs)) {
+  if (attend_unit<DQK, QT, STREAM, KV8, false>(u, sm, a, q, addr_list, scale_list, ncmp, sinks, plan,
+                                               out, lse, ws_o, ws_ml, m_obs)) {
     lds_barrier();  // every wave is done with the ring before the redo refills it
-    attend_unit<DQK, QT, STREAM, true>(u, sm, a, q, addr_list, ncmp, sinks, plan, out, lse, ws_o,
-                                       ws_ml, m_obs);
+    attend_unit<DQK, QT, STREAM, KV8, true>(u, sm, a, q, addr_list, scale_list, ncmp, sinks, plan,
+                                            out, lse, ws_o, ws_ml, m_obs);
   }
 }
 

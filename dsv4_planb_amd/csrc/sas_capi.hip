@@ -98,6 +98,7 @@ int check_tensors(const sas_params_t* p, const sas_tensors_t* t) {
 struct Ws {
   int* rows;
   uint64_t* addr;
+  float* scale;  // fp8 KV only
   int* ncmp;
   int* plan;
   float* o;
@@ -107,12 +108,13 @@ struct Ws {
 int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out) {
   const SasWsLayout W = sas_ws_layout(p->total_tokens, list_k(p),
                                       p->num_heads_q, p->head_dim_v, target, p->scenario,
-                                      p->ori_win_left);
+                                      p->ori_win_left, p->kv_dtype == SAS_DT_FP8E4M3);
   if (!ws || ws_bytes < W.total) return SAS_ERR_WORKSPACE;
   if (((uintptr_t)ws & 255u) != 0) return SAS_ERR_WORKSPACE;
   char* base = static_cast<char*>(ws);
   out->rows = reinterpret_cast<int*>(base + W.off_rows);
   out->addr = reinterpret_cast<uint64_t*>(base + W.off_addr);
+  out->scale = p->kv_dtype == SAS_DT_FP8E4M3 ? reinterpret_cast<float*>(base + W.off_scale) : nullptr;
   out->ncmp = reinterpret_cast<int*>(base + W.off_ncmp);
   out->plan = reinterpret_cast<int*>(base + W.off_plan);
   out->o = reinterpret_cast<float*>(base + W.off_o);
@@ -120,42 +122,17 @@ int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out)
   return SAS_OK;
 }
 
-typedef void (*fwd_fn_t)(SasFwdArgs, const uint16_t*, const uint8_t*, const uint8_t*,
-                         const float*, const float*, const int*, const int*, const int*,
-                         const int*, const float*, const int*, uint16_t*, float*, float*, float*);
+typedef void (*attend_fn_t)(SasFwdArgs, const uint16_t*, const uint64_t*, const float*,
+                            const int*, const float*, const int*, uint16_t*, float*, float*, float*);
 
-template <int NW, int DQK, int QT, bool KV8>
-fwd_fn_t fwd_ptr() {
-  return &sas::fwd_kernel<NW, DQK, QT, KV8>;
-}
-
-template <int NW, int DQK>
-fwd_fn_t pick_dtype(int qt, bool kv8) {
-  if (qt == 0) return kv8 ? fwd_ptr<NW, DQK, 0, true>() : fwd_ptr<NW, DQK, 0, false>();
-  return kv8 ? fwd_ptr<NW, DQK, 1, true>() : fwd_ptr<NW, DQK, 1, false>();
-}
-
-template <int NW>
-fwd_fn_t pick_dqk(int dqk, int qt, bool kv8) {
-  return dqk == 576 ? pick_dtype<NW, 576>(qt, kv8) : pick_dtype<NW, 512>(qt, kv8);
-}
-
-fwd_fn_t pick_fwd(const sas_params_t* p) {
-  const int qt = p->q_dtype == SAS_DT_BF16 ? 0 : 1;
-  const bool kv8 = p->kv_dtype == SAS_DT_FP8E4M3;
-  const int nw = (p->num_heads_q + 31) / 32;
-  if (nw <= 1) return pick_dqk<1>(p->head_dim_qk, qt, kv8);
-  if (nw == 2) return pick_dqk<2>(p->head_dim_qk, qt, kv8);
-  return pick_dqk<4>(p->head_dim_qk, qt, kv8);
-}
-
-typedef void (*attend_fn_t)(SasFwdArgs, const uint16_t*, const uint8_t*, const uint8_t*,
-                            const int*, const uint64_t*, const int*, const float*, const int*,
-                            uint16_t*, float*, float*, float*);
-
-template <int DQK, bool NT>
+template <int DQK, bool NT, bool KV8>
 attend_fn_t attend_ptr(bool f16) {
-  return f16 ? &sas::attend_kernel<DQK, 1, NT> : &sas::attend_kernel<DQK, 0, NT>;
+  return f16 ? &sas::attend_kernel<DQK, 1, NT, KV8> : &sas::attend_kernel<DQK, 0, NT, KV8>;
+}
+
+template <int DQK, bool KV8>
+attend_fn_t attend_ptr(bool f16, bool nt) {
+  return nt ? attend_ptr<DQK, true, KV8>(f16) : attend_ptr<DQK, false, KV8>(f16);
 }
 
 // Decode-like calls (at most 4 query tokens per sequence on average) read each KV
@@ -164,8 +141,10 @@ attend_fn_t attend_ptr(bool f16) {
 attend_fn_t pick_attend(const sas_params_t* p) {
   const bool f16 = p->q_dtype == SAS_DT_FP16;
   const bool nt = (int64_t)p->total_tokens <= 4 * (int64_t)p->batch;
-  if (p->head_dim_qk == 576) return nt ? attend_ptr<576, true>(f16) : attend_ptr<576, false>(f16);
-  return nt ? attend_ptr<512, true>(f16) : attend_ptr<512, false>(f16);
+  const bool kv8 = p->kv_dtype == SAS_DT_FP8E4M3;
+  if (p->head_dim_qk == 576)
+    return kv8 ? attend_ptr<576, true>(f16, nt) : attend_ptr<576, false>(f16, nt);
+  return kv8 ? attend_ptr<512, true>(f16, nt) : attend_ptr<512, false>(f16, nt);
 }
 
 int launch_status() { return hipGetLastError() == hipSuccess ? SAS_OK : SAS_ERR_LAUNCH; }
@@ -249,8 +228,9 @@ int sas_workspace_size(const sas_params_t* p, size_t* bytes) {
   int rc = sas_validate(p);
   if (rc) return rc;
   if (!bytes) return SAS_ERR_NULL;
-  *bytes = sas_ws_layout(p->total_tokens, list_k(p), p->num_heads_q,
-                         p->head_dim_v, target_units(p), p->scenario, p->ori_win_left)
+  *bytes = sas_ws_layout(p->total_tokens, list_k(p), p->num_heads_q, p->head_dim_v,
+                         target_units(p), p->scenario, p->ori_win_left,
+                         p->kv_dtype == SAS_DT_FP8E4M3)
                .total;
   return SAS_OK;
 }
@@ -281,7 +261,7 @@ int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
                      (hipStream_t)stream, fwd_args(p, target), plan, t->ori_block_table,
                      t->cmp_sparse_indices, t->cmp_block_table, w.rows, w.ncmp, w.addr,
                      static_cast<const uint8_t*>(t->ori_kv), static_cast<const uint8_t*>(t->cmp_kv),
-                     p->kv_dtype == SAS_DT_FP8E4M3 ? 1 : 2);
+                     p->kv_dtype == SAS_DT_FP8E4M3 ? 1 : 2, t->ori_kv_scale, t->cmp_kv_scale, w.scale);
   return launch_status();
 }
 
@@ -296,18 +276,8 @@ int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pla
   if (!plan) plan = w.plan;
   if (p->total_tokens == 0) return SAS_OK;
   const SasFwdArgs a = fwd_args(p, target);
-  if (p->kv_dtype != SAS_DT_FP8E4M3) {
-    hipLaunchKernelGGL(pick_attend(p), dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream, a,
-                       static_cast<const uint16_t*>(t->q), static_cast<const uint8_t*>(t->ori_kv),
-                       static_cast<const uint8_t*>(t->cmp_kv), t->cmp_block_table, w.addr,
-                       w.ncmp, t->sinks, plan, static_cast<uint16_t*>(t->out), t->lse, w.o, w.ml);
-    return launch_status();
-  }
-  fwd_fn_t fn = pick_fwd(p);
-  hipLaunchKernelGGL(fn, dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream, a,
-                     static_cast<const uint16_t*>(t->q), static_cast<const uint8_t*>(t->ori_kv),
-                     static_cast<const uint8_t*>(t->cmp_kv), t->ori_kv_scale, t->cmp_kv_scale,
-                     t->ori_block_table, t->cmp_block_table, w.rows, w.ncmp, t->sinks, plan,
+  hipLaunchKernelGGL(pick_attend(p), dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream, a,
+                     static_cast<const uint16_t*>(t->q), w.addr, w.scale, w.ncmp, t->sinks, plan,
                      static_cast<uint16_t*>(t->out), t->lse, w.o, w.ml);
   return launch_status();
 }
@@ -364,7 +334,8 @@ int sas_debug_rows(const sas_params_t* p, const void* ws, int32_t* rows, int32_t
   if (!ws || !rows || !counts) return SAS_ERR_NULL;
   const int K = list_k(p);
   const SasWsLayout W = sas_ws_layout(p->total_tokens, K, p->num_heads_q, p->head_dim_v,
-                                      target_units(p), p->scenario, p->ori_win_left);
+                                      target_units(p), p->scenario, p->ori_win_left,
+                                      p->kv_dtype == SAS_DT_FP8E4M3);
   const size_t stride = (size_t)sas_row_list_stride(p->ori_win_left, K, p->scenario);
   const char* base = static_cast<const char*>(ws);
   if (hipMemcpyAsync(rows, base + W.off_rows, (size_t)p->total_tokens * stride * 4,

@@ -54,7 +54,7 @@ SAS_HD static inline SasPlanLayout sas_plan_layout(int64_t T, int64_t target) {
 
 // ---- workspace (bytes, each region 256-B aligned) ----
 struct SasWsLayout {
-  size_t off_rows, off_addr, off_ncmp, off_plan, off_o, off_ml, total;
+  size_t off_rows, off_addr, off_scale, off_ncmp, off_plan, off_o, off_ml, total;
   int64_t slot_cap;
 };
 
@@ -68,7 +68,8 @@ SAS_HD static inline int64_t sas_row_list_stride(int64_t win_left, int64_t K, in
 }
 
 SAS_HD static inline SasWsLayout sas_ws_layout(int64_t T, int64_t K, int64_t H, int64_t Dv,
-                                        int64_t target, int scenario, int64_t win_left) {
+                                        int64_t target, int scenario, int64_t win_left,
+                                        bool kv8) {
   SasWsLayout W;
   size_t off = 0;
   W.off_rows = off;
@@ -78,6 +79,11 @@ SAS_HD static inline SasWsLayout sas_ws_layout(int64_t T, int64_t K, int64_t H, 
   W.off_addr = off;
   off = sas_align256(off + ((size_t)(T > 0 ? T : 1) * sas_row_list_stride(win_left, K, scenario) +
                             SAS_TILE) * 8);
+  // fp8 KV: the fp32 dequantisation scale s of every listed row, then a second list
+  // of 1 / s (0 where s = 0), same shape
+  W.off_scale = off;
+  if (kv8)
+    off = sas_align256(off + 2 * (size_t)(T > 0 ? T : 1) * sas_row_list_stride(win_left, K, scenario) * 4);
   W.off_ncmp = off;
   off = sas_align256(off + (size_t)(T > 0 ? T : 1) * 4);
   W.off_plan = off;

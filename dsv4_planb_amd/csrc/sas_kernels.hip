@@ -8,12 +8,8 @@
 //                   examine the first min(K, thr) slots, -1 terminates, ids >= thr
 //                   are skipped, survivors are compacted in slot order and mapped
 //                   through the paged block table to pool rows.
-//   fwd_kernel      per work unit: gather paged KV rows into LDS, S^T = K Q^T and
-//                   O^T += V^T P^T on bf16/fp16 MFMA (32x32x16) with fp32
-//                   accumulation, one sink-seeded online softmax across the window
-//                   and compressed rows (golden.py:156-200); writes the final
-//                   output or an un-normalised split partial (O, m, l).
 //   combine_kernel  log-sum-exp merge of split partials.
+// The attention kernel itself (bf16 / fp16 and fp8 KV) is in sas_attend.hip.
 //
 // Work decomposition: one work unit = (token, contiguous range of its row list);
 // the row list of a token is its window rows (raw KV pool) followed by its
@@ -238,7 +234,10 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
                                                         uint64_t* __restrict__ addr_out,
                                                         const uint8_t* __restrict__ ori_kv,
                                                         const uint8_t* __restrict__ cmp_kv,
-                                                        int esz) {
+                                                        int esz,
+                                                        const float* __restrict__ ori_scale,
+                                                        const float* __restrict__ cmp_scale,
+                                                        float* __restrict__ scale_out) {
   __shared__ int s_wmin[RS_NT / 64];
   __shared__ int s_wsum[RS_NT / 64];
   __shared__ int s_cbt[RS_CBT_LDS];
@@ -276,6 +275,16 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
   }
   int* out = rows_out + (size_t)t * a.list_stride;
   uint64_t* aout = addr_out + (size_t)t * a.list_stride;
+  // fp8 KV: each row's dequantisation scale s and 1 / s beside its address (a -1
+  // code reads the zero row: s = 1, so that its P counts in the output normaliser
+  // as a zero row of a 16-bit pool does)
+  float* sout = scale_out ? scale_out + (size_t)t * a.list_stride : nullptr;
+  const size_t inv_off = (size_t)a.T * a.list_stride;  // the 1 / s list follows the s list
+  auto put_scale = [&](int r, int code, const float* __restrict__ sc) {
+    const float s = code < 0 ? 1.f : sc[code];
+    sout[r] = s;
+    sout[inv_off + r] = s != 0.f ? 1.f / s : 0.f;
+  };
   const int nwin = tk[TK_NWIN], winlo = tk[TK_WINLO];
   // Second: the window's block-table entries and the batch's compressed block-table
   // row, staged in LDS so the per-id page lookups below stay on chip.
@@ -288,8 +297,10 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     const int code = paged_code(obt, a.ori_table_len, a.ori_block_size, a.ori_block_num, winlo + r);
     out[r] = code;
     aout[r] = code_addr(code, ori_kv, a.ori_block_size, a.ori_block_stride, a.ori_row_stride, esz);
+    if (sout) put_scale(r, code, ori_scale);
   }
   aout += nwin;
+  if (sout) sout += nwin;
   if (a.scenario == 1) {
     if (tid == 0) ncmp_out[t] = 0;
     return;
@@ -304,6 +315,7 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
       const int code = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, j);
       out[j] = code;
       aout[j] = code_addr(code, cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
+      if (sout) put_scale(j, code, cmp_scale);
     }
     if (tid == 0) ncmp_out[t] = n;
     return;
@@ -363,6 +375,7 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
       if ((keep >> k) & 1u) {
         const int code = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, v[k]);
         out[pos] = code;
+        if (sout) put_scale(pos, code, cmp_scale);
         aout[pos++] = code_addr(code, cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
       }
     emitted += total;
@@ -373,18 +386,8 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
 }
 
 // ===========================================================================
-// Attention
+// 16-bit conversions (attention and combine kernels)
 // ===========================================================================
-template <int QT>
-__device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
-  if constexpr (QT == 0)
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
-                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-}
-
 // float -> 16-bit payload of the query dtype, round to nearest even.
 template <int QT>
 __device__ __forceinline__ uint32_t to_q16(float x) {
@@ -509,348 +512,8 @@ __device__ __forceinline__ void combine_head(int t, int h, int H, int S, int bas
   if (lse && lane == 0) lse[(size_t)t * H + h] = (mx + __log2f(le)) * 0.6931471805599453f;
 }
 
-// OCP FP8 E4M3FN code -> exact 16-bit value of the query dtype.
-template <int QT>
-__device__ __forceinline__ uint32_t fp8_to_q16(uint32_t v) {
-  const uint32_t e = (v >> 3) & 15u, m = v & 7u;
-  const uint32_t s = (v & 0x80u) << 8;
-  if constexpr (QT == 0) {
-    if (e == 15u && m == 7u) return s | 0x7FC0u;
-    if (e == 0u) return m == 0u ? s : (s | (__float_as_uint((float)m * 0.001953125f) >> 16));
-    return s | ((e + 120u) << 7) | (m << 4);
-  } else {
-    if (e == 15u && m == 7u) return s | 0x7E00u;
-    if (e == 0u)
-      return m == 0u ? s
-                     : (s | (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)((float)m * 0.001953125f)));
-    return s | ((e + 8u) << 10) | (m << 7);
-  }
-}
-
-// Source of rows that read as zeros (unused pages, tile padding).
-
-
-// Online softmax (golden.py:184-196): m_run is the running maximum of the sink
-// and every logit seen so far; a tile whose maximum exceeds it rescales O and l
-// by 2^(m_old - m_new) before P = 2^(x - m_run) is formed, so P <= 1 and the
-// row holding the maximum gets P = 1 exactly, as in the reference.  The rescale
-// runs only when some head of the wave saw a larger maximum.
+// log2(e): logits are kept in log2 units (scale_log2 = softmax_scale * log2(e)).
 constexpr float LOG2E = 1.4426950408889634f;
-
-template <int NW, int DQK, int QT, bool KV8>
-__global__ __launch_bounds__(256, 1) void fwd_kernel(
-    SasFwdArgs a, const uint16_t* __restrict__ q, const uint8_t* __restrict__ ori_kv,
-    const uint8_t* __restrict__ cmp_kv, const float* __restrict__ ori_scale,
-    const float* __restrict__ cmp_scale, const int* __restrict__ ori_bt,
-    const int* __restrict__ cmp_bt, const int* __restrict__ rows_list,
-    const int* __restrict__ ncmp, const float* __restrict__ sinks, const int* __restrict__ plan,
-    uint16_t* __restrict__ out, float* __restrict__ lse, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml) {
-  constexpr int DV = 512;
-  constexpr int NT = 256;
-  constexpr int ROWB = DQK * 2;          // LDS row bytes (16-bit elements)
-  constexpr int CPR = ROWB / 16;         // 16-B chunks per LDS row: 72 / 64
-  constexpr int KSTEPS = DQK / 16;       // MFMA k-steps of Q K^T
-  constexpr int TILEB = SAS_TILE * ROWB;
-  constexpr int NBUF = KV8 ? 1 : 2;      // DMA path double-buffers; fp8 stages through VGPRs
-  constexpr int ESZ = KV8 ? 1 : 2;       // source element bytes
-  constexpr int CPT = SAS_TILE * CPR / NT;  // DMA chunks per thread per tile (9 / 8)
-  static_assert(SAS_TILE * CPR % NT == 0, "tile must split evenly over the workgroup");
-  constexpr int SRC_CPR8 = DQK / 16;     // fp8: 16-B source chunks per row (36 / 32)
-  constexpr int CPT8 = (SAS_TILE * SRC_CPR8 + NT - 1) / NT;
-
-  __shared__ __attribute__((aligned(16))) uint8_t tiles[NBUF * TILEB];
-  __shared__ const uint8_t* rowaddr[2][SAS_TILE];
-  __shared__ float rowscale[SAS_TILE];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = tid >> 6;
-  const int g = lane >> 5;   // half-wave: selects the k-chunk / key quad
-  const int li = lane & 31;  // MFMA row/column index within the 32-wide tile
-
-  const int u = blockIdx.x;
-  if (plan[PH_MAGIC] != SAS_PLAN_MAGIC || u >= plan[PH_UNITS]) return;
-  const int* ur = plan + SAS_PLAN_HDR + (size_t)SAS_TOK_W * a.T + (size_t)u * SAS_UNIT_W;
-  const int t = ur[0], split = ur[3];
-  const int H = a.H;
-
-  if (split < 0) {  // a q row no batch owns: zeros, as the reference's padded slots
-    for (int i = tid; i < H * DV / 8; i += NT)
-      reinterpret_cast<u32x4_t*>(out + (size_t)t * H * DV)[i] = u32x4_t{0, 0, 0, 0};
-    if (lse)
-      for (int i = tid; i < H; i += NT) lse[(size_t)t * H + i] = 0.f;
-    return;
-  }
-
-  const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
-  const int nwin = tk[TK_NWIN];
-  const int splits = tk[TK_SPLITS], wsbase = tk[TK_WSBASE];
-  const int r0 = ur[1];
-  const int r1 = min(ur[2], nwin + ncmp[t]);
-  const int ntiles = r1 > r0 ? (r1 - r0 + SAS_TILE - 1) / SAS_TILE : 0;
-  const int* codes = rows_list + (size_t)t * a.list_stride;
-
-  // Row code of list row r (-1 = zero row); window rows first, then compressed rows.
-  auto row_code = [&](int r) -> int { return r < r1 ? codes[r] : -1; };
-  auto row_ptr = [&](int r, int code) -> const uint8_t* {
-    if (code < 0) return g_zero_row;
-    if (r < nwin) {
-      const int page = code / a.ori_block_size, off = code - page * a.ori_block_size;
-      return ori_kv + ((size_t)page * a.ori_block_stride + (size_t)off * a.ori_row_stride) * ESZ;
-    }
-    const int page = code / a.cmp_block_size, off = code - page * a.cmp_block_size;
-    return cmp_kv + ((size_t)page * a.cmp_block_stride + (size_t)off * a.cmp_row_stride) * ESZ;
-  };
-  auto row_scale = [&](int r, int code) -> float {
-    if (code < 0) return 0.f;
-    return r < nwin ? ori_scale[code] : cmp_scale[code];
-  };
-
-  // ---- LDS addressing ----
-  // Row-major tile; 16-B chunk c of row r lives at chunk (c ^ (r & 7)) of that row,
-  // so each ds_read_b128 phase (8 lanes) and ds_read_b32 phase (32 lanes) hits
-  // distinct banks.  Every operand read is a per-lane base plus a constant:
-  //  * K, k-step ks: row li, chunk 2 ks + g            = kbase[ks & 3] + 128 (ks >> 2)
-  //  * V^T, block pair mm, k-step kk, element e: row 16 kk + 8 (e >> 2) + 4 g + (e & 3),
-  //    dword 32 mm + li                                 = vbase[e & 3] + (16 kk + 8 (e >> 2)) ROWB + 128 mm
-  uint32_t kbase[4], vbase[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    kbase[j] = li * ROWB + (((2 * j + g) ^ (li & 7)) * 16);
-    vbase[j] = (4 * g + j) * ROWB + 16 * ((li >> 2) ^ (4 * g + j)) + 4 * (li & 3);
-  }
-
-  // ---- per-wave state: 32 heads per wave ----
-  // Every wave computes (no divergence around the register tiles); head indices
-  // past H (and waves past NW) are clamped onto valid heads and never stored.
-  const int h = w * 32 + li;
-  const bool hvalid = (w < NW) && (h < H);
-  const int hc = min(h, H - 1);
-  u32x4_t qf[KSTEPS];
-  {
-    const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(q + ((size_t)t * H + hc) * DQK);
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) qf[ks] = qrow[2 * ks + g];
-  }
-  const float sink2 = split == 0 ? sinks[hc] * LOG2E : -INFINITY;  // golden.py:162-163
-  f32x16_t acc[16];
-  float m_run = sink2, l_run = split == 0 ? 1.f : 0.f;  // golden.py:162-163
-
-  // fp8: 16 source bytes -> two 16-bit chunks written to the (single) tile
-  auto fp8_stage = [&](int it) {
-    u32x4_t st[CPT8];
-#pragma unroll
-    for (int k = 0; k < CPT8; ++k) {
-      const int c = tid + k * NT;
-      const int cc = c < SAS_TILE * SRC_CPR8 ? c : 0;
-      const int row = cc / SRC_CPR8, chk = cc - row * SRC_CPR8;
-      st[k] = *reinterpret_cast<const u32x4_t*>(rowaddr[it & 1][row] + chk * 16);
-    }
-#pragma unroll
-    for (int k = 0; k < CPT8; ++k) {
-      const int c = tid + k * NT;
-      if (c < SAS_TILE * SRC_CPR8) {
-        const int row = c / SRC_CPR8, chk = c - row * SRC_CPR8;
-#pragma unroll
-        for (int hlf = 0; hlf < 2; ++hlf) {
-          const uint32_t w0 = st[k][2 * hlf], w1 = st[k][2 * hlf + 1];
-          u32x4_t o;
-          o[0] = fp8_to_q16<QT>(w0 & 0xff) | (fp8_to_q16<QT>((w0 >> 8) & 0xff) << 16);
-          o[1] = fp8_to_q16<QT>((w0 >> 16) & 0xff) | (fp8_to_q16<QT>(w0 >> 24) << 16);
-          o[2] = fp8_to_q16<QT>(w1 & 0xff) | (fp8_to_q16<QT>((w1 >> 8) & 0xff) << 16);
-          o[3] = fp8_to_q16<QT>((w1 >> 16) & 0xff) | (fp8_to_q16<QT>(w1 >> 24) << 16);
-          const int ch = 2 * chk + hlf;
-          *reinterpret_cast<u32x4_t*>(tiles + row * ROWB + ((ch ^ (row & 7)) * 16)) = o;
-        }
-      }
-    }
-  };
-  // 16-bit KV: each lane DMAs 16 B of the tile straight into LDS.  Wave w's k-th
-  // instruction fills LDS chunk slots [(4k + w) * 64, +64): slot s holds chunk
-  // (s % CPR) ^ (row & 7) of row s / CPR.
-  auto dma_tile = [&](int buf, int slot) {
-    uint8_t* dst0 = tiles + buf * TILEB;
-    // Recomputed per tile (an opaque copy of the lane id stops the compiler from
-    // hoisting 2 x CPT loop-invariant VGPRs out of the tile loop).
-    int lane_v = lane;
-    asm volatile("" : "+v"(lane_v));
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int s = (4 * k + w) * 64 + lane_v;
-      const int row = s / CPR, pc = s - row * CPR;
-      const uint8_t* src = rowaddr[slot][row] + ((pc ^ (row & 7)) * 16);
-      __builtin_amdgcn_global_load_lds(
-          (const void*)src,
-          (__attribute__((address_space(3))) void*)(dst0 + (4 * k + w) * 64 * 16), 16, 0, 0);
-    }
-  };
-
-  {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = f32x16_t{};
-
-    // prologue: addresses of tiles 0 and 1; DMA of tile 0
-    if (tid < SAS_TILE) {
-      for (int j = 0; j < 2; ++j) {
-        const int r = r0 + j * SAS_TILE + tid;
-        const int code = row_code(r);
-        rowaddr[j][tid] = row_ptr(r, code);
-        if (KV8 && j == 0) rowscale[tid] = row_scale(r, code);
-      }
-    }
-    __syncthreads();
-    if (!KV8 && ntiles > 0) dma_tile(0, 0);
-
-    for (int it = 0; it < ntiles; ++it) {
-      const int buf = KV8 ? 0 : (it & 1);
-      __syncthreads();  // all waves are done with tile it-1 (and its buffer)
-      int code2 = -1;
-      const int r2 = r0 + (it + 2) * SAS_TILE + tid;
-      if (tid < SAS_TILE) code2 = row_code(r2);  // issued before the next DMA: ready at the wait
-      if constexpr (!KV8) {
-        if (it + 1 < ntiles) {
-          dma_tile((it + 1) & 1, (it + 1) & 1);
-          asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CPT) : "memory");
-        } else {
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-        if (tid < SAS_TILE) rowaddr[it & 1][tid] = row_ptr(r2, code2);
-      } else {
-        fp8_stage(it);
-      }
-      __syncthreads();  // tile it is in LDS for every wave
-      const uint8_t* tile = tiles + buf * TILEB;
-      const int nvalid = min(SAS_TILE, r1 - (r0 + it * SAS_TILE));
-
-      // ---- S^T[key][head] = K Q^T : A = K rows (LDS), B = Q^T (registers) ----
-      f32x16_t s = f32x16_t{};
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        const u32x4_t kf =
-            *reinterpret_cast<const u32x4_t*>(tile + kbase[ks & 3] + (ks >> 2) * 128);
-        s = mfma32<QT>(kf, qf[ks], s);
-      }
-      // C layout: register r holds key 8 (r / 4) + 4 g + r % 4 for head li.
-      float x[16];
-      float mt = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = 8 * (r >> 2) + 4 * g + (r & 3);
-        float v = s[r] * a.scale_log2;
-        if (KV8) v *= rowscale[key];
-        x[r] = key < nvalid ? v : -INFINITY;
-        mt = fmaxf(mt, x[r]);
-      }
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      if (__any(mt > m_run)) {  // golden.py:185-187,196: rescale O and l to the new maximum
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = m_new > m_run ? exp2f(m_run - m_new) : 1.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] *= alpha;
-        l_run *= alpha;
-        m_run = m_new;
-      }
-      float ps = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        x[r] = exp2f(x[r] - m_run);
-        ps += x[r];
-      }
-      ps += __shfl_xor(ps, 32);
-      l_run += ps;
-      // P^T as the B operand: k-step kk element e = register 8 kk + e.
-      u32x4_t pk[2];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float p0 = x[8 * kk + 2 * e], p1 = x[8 * kk + 2 * e + 1];
-          if (KV8) {  // V = fp8 * scale: fold the row scale into P
-            p0 *= rowscale[16 * kk + 8 * ((2 * e) >> 2) + 4 * g + ((2 * e) & 3)];
-            p1 *= rowscale[16 * kk + 8 * ((2 * e + 1) >> 2) + 4 * g + ((2 * e + 1) & 3)];
-          }
-          pk[kk][e] = to_q16<QT>(p0) | (to_q16<QT>(p1) << 16);
-        }
-      }
-      // ---- O^T[d][head] += V^T P^T : A = V^T gathered from the row-major tile ----
-      // Block pair mm covers d in [64 mm, 64 mm + 64): MFMA row li of block 2 mm + j
-      // is d = 64 mm + 2 li + j, so one dword per key feeds both blocks of the pair.
-#pragma unroll
-      for (int mm = 0; mm < 8; ++mm) {
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          uint32_t wv[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            wv[e] = *reinterpret_cast<const uint32_t*>(
-                tile + vbase[e & 3] + (16 * kk + 8 * (e >> 2)) * ROWB + 128 * mm);
-          u32x4_t a0, a1;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            a0[e] = __builtin_amdgcn_perm(wv[2 * e + 1], wv[2 * e], 0x05040100u);
-            a1[e] = __builtin_amdgcn_perm(wv[2 * e + 1], wv[2 * e], 0x07060302u);
-          }
-          acc[2 * mm] = mfma32<QT>(a0, pk[kk], acc[2 * mm]);
-          acc[2 * mm + 1] = mfma32<QT>(a1, pk[kk], acc[2 * mm + 1]);
-        }
-      }
-      if constexpr (KV8) {
-        __syncthreads();  // tile and scales consumed; next tile's scales may be written
-        if (tid < SAS_TILE && it + 1 < ntiles) {
-          const int r = r0 + (it + 1) * SAS_TILE + tid;
-          const int code = row_code(r);
-          rowaddr[(it + 1) & 1][tid] = row_ptr(r, code);
-          rowscale[tid] = row_scale(r, code);
-        }
-      }
-    }
-  }
-
-  // ---- epilogue ----
-  if (!hvalid) return;
-  if (splits == 1) {
-    const float inv = 1.f / l_run;
-    uint16_t* orow = out + ((size_t)t * H + h) * DV;
-#pragma unroll
-    for (int mm = 0; mm < 8; ++mm) {
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        // registers 4 q4 .. 4 q4 + 3 of blocks 2 mm, 2 mm + 1 -> d = 64 mm + 16 q4 + 8 g + [0, 8)
-        u32x4_t o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          o[e] = to_q16<QT>(acc[2 * mm][4 * q4 + e] * inv) |
-                 (to_q16<QT>(acc[2 * mm + 1][4 * q4 + e] * inv) << 16);
-        *reinterpret_cast<u32x4_t*>(orow + 64 * mm + 16 * q4 + 8 * g) = o;
-      }
-    }
-    if (lse && g == 0) lse[(size_t)t * H + h] = (m_run + __log2f(l_run)) * 0.6931471805599453f;
-  } else {
-    const int slot = wsbase + split;
-    float* orow = ws_o + ((size_t)slot * H + h) * DV;
-#pragma unroll
-    for (int mm = 0; mm < 8; ++mm) {
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        float4 v0, v1;
-        v0.x = acc[2 * mm][4 * q4 + 0];
-        v0.y = acc[2 * mm + 1][4 * q4 + 0];
-        v0.z = acc[2 * mm][4 * q4 + 1];
-        v0.w = acc[2 * mm + 1][4 * q4 + 1];
-        v1.x = acc[2 * mm][4 * q4 + 2];
-        v1.y = acc[2 * mm + 1][4 * q4 + 2];
-        v1.z = acc[2 * mm][4 * q4 + 3];
-        v1.w = acc[2 * mm + 1][4 * q4 + 3];
-        float4* dst = reinterpret_cast<float4*>(orow + 64 * mm + 16 * q4 + 8 * g);
-        dst[0] = v0;
-        dst[1] = v1;
-      }
-    }
-    if (g == 0)
-      reinterpret_cast<float4*>(ws_ml)[(size_t)slot * H + h] = make_float4(m_run, l_run, l_run, 0.f);
-  }
-}
 
 // ===========================================================================
 // Split combine: one wave per (split token, head), grid-stride over the split

@@ -73,6 +73,16 @@ def assert_parity(out, lse, ref_out, ref_lse, dtype="bf16", max_abs=2e-2, mean_a
       its first tile's), so where several rows carry comparable weight their
       rounding errors differ at the 2^-9 level (the reference's own device
       kernel, with 128-row tiles, is in the same position).
+    * ``rule="reference_fp8"``: the reference rule for fp8 e4m3 KV, with 1 point of
+      slack against the oracle's count and 98% against the oracle directly.  The
+      device folds each row's fp32 scale into P before rounding (bf16(P s) times
+      the e4m3 row), where the oracle rounds P and multiplies the fp32
+      dequantised row, so the dominant row's weight is rounded too.  On the
+      reference's large-magnitude draws that moves about half a percent of the
+      elements across the rtol / atol boundary while the error against the exact
+      value stays the oracle's (the bounds below); with one common frame the
+      oracle's own rounding scheme passes 99.18% of the stress case's elements
+      and this one 98.76%, so a 0.1-point slack is below the rounding noise.
     * with ``exact`` (the float64 one-shot softmax over the same rows): the
       device error against the exact value is at most 1.25x the oracle's own
       error on average and 2x at the worst element (plus one bf16 ulp of
@@ -103,8 +113,9 @@ def assert_parity(out, lse, ref_out, ref_lse, dtype="bf16", max_abs=2e-2, mean_a
         gful, grel = check_result_rule(ref_out, exact[0], dtype)
         msg += f" | vs exact: dev {dful:.3f}%/{drel:.2f} oracle {gful:.3f}%/{grel:.2f}"
         print(msg, flush=True)
-        assert dful >= min(99.5, gful - 0.1) and drel < 10.0, msg
-        assert ful >= 99.0 and rel < 10.0, msg
+        slack, floor = (1.0, 98.0) if rule == "reference_fp8" else (0.1, 99.0)
+        assert dful >= min(99.5, gful - slack) and drel < 10.0, msg
+        assert ful >= floor and rel < 10.0, msg
     assert lful >= 99.5 and lrel < 10.0, msg
     if exact is not None and ek.size:
         assert ek.mean() <= 1.25 * eg.mean() + 1e-7, msg

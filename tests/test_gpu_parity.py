@@ -71,6 +71,43 @@ def test_c5_ragged_fp8_reduced():
     _check("c5[B=8,fp8]", c)
 
 
+# ---- fp8 e4m3 KV (per-row fp32 scales): every path of the kernel's fp8 variant ----
+def _fp8_edges():
+    c = make_case(B=4, H=32, seq_kv=[900, 3000, 2, 64], q_per_seq=[2, 3, 3, 1], scenario=3, K=256,
+                  kv_dtype="fp8e4m3", seed=21)
+    c.idx[0, 3] = -1
+    c.idx[1, 0] = 10_000
+    c.ori_block_table[1, 2] = -1  # an unused page in a window: zero rows, scale 0
+    return c
+
+
+@pytest.mark.parametrize("name,build,extra,rule", [
+    ("fp8_swa", lambda: make_case(B=2, H=16, seq_kv=[1024, 1500], q_per_seq=[1, 2], scenario=1,
+                                  kv_dtype="fp8e4m3", seed=22), {}, "baseline"),
+    ("fp8_cfa", lambda: make_case(B=1, H=64, seq_kv=[8193], q_per_seq=1, scenario=2, K=0,
+                                  cmp_ratio=128, block_size=128, cmp_block_size=128,
+                                  kv_dtype="fp8e4m3", seed=23), {}, "baseline"),
+    ("fp8_d512", lambda: make_case(B=2, H=128, D=512, seq_kv=[5000, 12000], q_per_seq=2,
+                                   scenario=3, K=1024, kv_dtype="fp8e4m3", seed=24), {}, "baseline"),
+    ("fp8_fp16q", lambda: make_case(B=3, H=64, seq_kv=[3000, 700, 9000], q_per_seq=[1, 2, 3],
+                                    scenario=3, K=512, q_dtype="fp16", kv_dtype="fp8e4m3",
+                                    seed=25), {}, "baseline"),
+    ("fp8_splits", lambda: make_case(B=2, H=16, seq_kv=[20000, 4000], q_per_seq=1, scenario=3,
+                                     K=2048, kv_dtype="fp8e4m3", seed=26),
+     {"core_num": 1024}, "baseline"),
+    ("fp8_edges", _fp8_edges, {}, "baseline"),
+    ("fp8_large_logits", lambda: make_case(B=2, H=128, seq_kv=[9000, 3000], q_per_seq=2,
+                                           scenario=3, K=1024, kv_dtype="fp8e4m3", seed=27,
+                                           dist="reference"), {}, "reference_fp8"),
+    ("fp8_prefill", lambda: make_case(B=1, H=128, seq_kv=[1024], q_per_seq=256, scenario=3,
+                                      K=512, kv_dtype="fp8e4m3", seed=28), {}, "baseline"),
+])
+def test_fp8_paths(name, build, extra, rule):
+    c = build()
+    toks = list(range(0, c.T, 5)) + [c.T - 1] if c.T > 64 else None
+    _check(name, c, tokens=toks, rule=rule, **extra)
+
+
 # ---- reference scenarios (test_sparse_attn_sharedkv.py:81-220): D=512, H=64, page 128,
 # the reference's own value draws (q / raw KV ~ U(-10,10), compressed KV ~ U(-5,10));
 # prefills at S1=1024 as in test_sparse_attn_sharedkv_fast.py ----
