@@ -10,6 +10,7 @@ window 128, compression ratio 4, d_qk 576, d_v 512, scale 1/sqrt(576)):
 * ``prefill8k``: one sequence, 8192 query tokens over 8192 KV, 128 heads, top-k
   2048 over the causally valid compressed rows (-1 padded).  MFMA-bound.
 * ``decode32``: B=32, 64 heads, KV lengths U[4096, 32768], top-k 512.
+* ``decode128k_fp8``: decode128k with the fp8 e4m3 pools of ``ragged_fp8``.
 * ``ragged_fp8``: B=64, KV lengths log-uniform in [256, 131072], 1, 2 or 4 query
   tokens per sequence, 128 heads, top-k 2048 (-1 padded where fewer compressed
   rows are valid); KV pools fp8 e4m3 with a per-row fp32 scale (580 B per row).
@@ -43,7 +44,9 @@ D_QK, D_V, PAGE, WIN, RATIO = 576, 512, 64, 128, 4
 ROW_BYTES = D_QK * 2
 ROW_BYTES_FP8 = D_QK + 4  # e4m3 payload + fp32 scale
 KERNEL_NAME = {"decode128k": "sas::attend_kernel<576, bf16>", "prefill8k": "sas::attend_kernel<576, bf16>",
-               "decode32": "sas::attend_kernel<576, bf16>", "ragged_fp8": "sas::fwd_kernel (fp8 e4m3 KV)"}
+               "decode32": "sas::attend_kernel<576, bf16>",
+               "decode128k_fp8": "sas::attend_kernel<576, bf16, fp8 KV>",
+               "ragged_fp8": "sas::attend_kernel<576, bf16, fp8 KV>"}
 FLOP_PER_ROW_HEAD = 2 * D_QK + 2 * D_V
 
 
@@ -75,10 +78,11 @@ def make_workload(name: str, seed: int = 0, dev="cuda", compact: bool = False):
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     fp8 = False
-    if name == "decode128k":
+    if name in ("decode128k", "decode128k_fp8"):
         B, q_per, H, ctx, K = 128, 2, 128, 131072, 2048
         kv = [ctx] * B
         q_lens = [q_per] * B
+        fp8 = name.endswith("fp8")
     elif name == "prefill8k":
         B, q_per, H, K = 1, 8192, 128, 2048
         kv = [8192]
@@ -481,7 +485,7 @@ def power_mode(name, secs, dev, compact=False):
 
 
 def main_r_batch(name):
-    return dict(decode128k=128, decode32=32, prefill8k=1, ragged_fp8=64)[name]
+    return dict(decode128k=128, decode32=32, prefill8k=1, decode128k_fp8=128, ragged_fp8=64)[name]
 
 
 # ---------------------------------------------------------------------------
@@ -491,8 +495,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="decode128k",
-                    choices=["decode128k", "prefill8k", "decode32", "ragged_fp8"])
-    ap.add_argument("--extra", default="prefill8k,decode32,ragged_fp8",
+                    choices=["decode128k", "prefill8k", "decode32", "decode128k_fp8", "ragged_fp8"])
+    ap.add_argument("--extra", default="prefill8k,decode32,decode128k_fp8,ragged_fp8",
                     help="comma-separated extra workloads reported under 'workloads' ('' = none)")
     ap.add_argument("--cpu-seqs", type=int, default=0,
                     help="cap on sampled sequences for the CPU baseline (0 = size for ~10 s)")
@@ -505,8 +509,8 @@ def main():
                          "--steps times (calibrates the HBM byte counters); power: --stage back "
                          "to back for --secs with a power / clock sample")
     ap.add_argument("--stage", default="decode128k",
-                    choices=["decode128k", "prefill8k", "decode32", "ragged_fp8", "mfma_probe",
-                             "read_probe"],
+                    choices=["decode128k", "prefill8k", "decode32", "decode128k_fp8", "ragged_fp8",
+                             "mfma_probe", "read_probe"],
                     help="what --mode power runs")
     ap.add_argument("--secs", type=float, default=10.0, help="--mode power duration")
     ap.add_argument("--compact", action="store_true",
@@ -577,7 +581,7 @@ def main():
                 "kernel": KERNEL_NAME[args.workload], "kernel_us": round(main_r["attend_us"], 2),
                 "algorithmic_bytes": main_r["alg_bytes"], "algorithmic_flops": main_r["alg_flops"]}
     cpu = None
-    if not args.no_cpu_baseline and args.workload != "ragged_fp8":
+    if not args.no_cpu_baseline and not args.workload.endswith("fp8"):
         _log("cpu baseline")
         if args.workload == "prefill8k":
             cpu = cpu_baseline(args.workload, 1)
@@ -593,6 +597,8 @@ def main():
                      "window 128, ratio 4, page 64, d_qk 576 / d_v 512",
         "decode32": "decode: B=32 seqs x U[4096,32768] KV, 1 query token, H=64, top-k 512, "
                     "window 128, ratio 4, page 64, d_qk 576 / d_v 512",
+        "decode128k_fp8": "decode: B=128 seqs x 131072 KV, 2 query tokens/seq, H=128, top-k 2048, "
+                          "window 128, ratio 4, page 64, fp8 e4m3 KV with per-row fp32 scale, bf16 q",
         "ragged_fp8": "ragged: B=64 seqs x log-U[256,131072] KV, 1/2/4 query tokens/seq, H=128, "
                       "top-k 2048 (-1 padded), window 128, ratio 4, page 64, fp8 e4m3 KV with "
                       "per-row fp32 scale, bf16 q",

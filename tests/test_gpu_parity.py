@@ -364,6 +364,32 @@ def test_device_plan_covers_every_row_once(cores):
     assert (used == 1).all(), "split workspace slots overlap or go unused"
 
 
+def _plan_units(q_lens, kv, K, cores):
+    from dsv4_planb_amd import metadata as M
+
+    B = len(q_lens)
+    cu = np.zeros(B + 1, np.int32)
+    cu[1:] = np.cumsum(q_lens)
+    plan = M.sparse_attn_sharedkv_metadata(
+        num_heads_q=128, num_heads_kv=1, head_dim=576, cu_seqlens_q=torch.from_numpy(cu).cuda(),
+        seqused_kv=torch.from_numpy(np.asarray(kv, np.int32)).cuda(), batch_size=B,
+        max_seqlen_q=int(max(q_lens)), max_seqlen_kv=int(max(kv)), cmp_topk=K, cmp_ratio=4,
+        layout_q="TND", has_cmp_kv=True, aic_core_num=cores)
+    torch.cuda.synchronize()
+    p = plan.cpu().numpy()
+    T, U, unit_cap = int(cu[-1]), int(p[3]), int(p[11])
+    units = p[M.PLAN_HDR + M.PLAN_TOK_W * T:][:M.PLAN_UNIT_W * unit_cap].reshape(unit_cap, M.PLAN_UNIT_W)[:U]
+    return units
+
+
+def test_device_plan_keeps_uniform_decode_unsplit():
+    """A uniform long decode batch (128 sequences x 131072, 2 query tokens, 256
+    CUs) gets one unit per token: nothing to balance and no partials to merge."""
+    print("\n[case] plan: uniform B=128 x 131072, 2 tokens", flush=True)
+    units = _plan_units([2] * 128, [131072] * 128, 2048, 256)
+    assert len(units) == 256 and (units[:, 3] == 0).all()
+
+
 # ---- hipGraph capture (reference test_graph_mode.py:107-209) ----
 @pytest.mark.parametrize("with_plan", [False, True])
 def test_graph_replays_match_eager(with_plan):
