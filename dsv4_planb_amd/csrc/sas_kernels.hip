@@ -221,6 +221,13 @@ __device__ __forceinline__ int paged_code(const int* __restrict__ bt_row, int ta
 // block-wide minimum) ends the list, ids outside [0, thr) are skipped, and the
 // survivors keep their slot order through a block-wide exclusive scan.
 constexpr int RS_NT = 256;
+
+// Workgroup barrier for the resolver: its threads exchange data only through LDS,
+// so it waits for LDS operations alone.  (__syncthreads() would also drain every
+// outstanding global load and store, putting their latency on each pass.)
+__device__ __forceinline__ void rs_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 constexpr int RS_PER = 8;  // index slots per thread and chunk
 
 constexpr int RS_CBT_LDS = 4096;  // compressed block-table entries staged in LDS
@@ -305,7 +312,7 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     if (tid == 0) ncmp_out[t] = 0;
     return;
   }
-  __syncthreads();  // s_cbt
+  rs_barrier();  // s_cbt
   const int* cbt = cbt_lds ? s_cbt : cbt_g;
   out += nwin;  // compressed codes follow the window codes
   const int thr = floor_div(tk[TK_SG] + 1, a.cmp_ratio);
@@ -342,7 +349,7 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) first = min(first, __shfl_xor(first, off));
     if (lane == 0) s_wmin[w] = first;
-    __syncthreads();
+    rs_barrier();
     int term = s_wmin[0];
 #pragma unroll
     for (int j = 1; j < RS_NT / 64; ++j) term = min(term, s_wmin[j]);
@@ -363,24 +370,52 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
       if (lane >= off) incl += x;
     }
     if (lane == 63) s_wsum[w] = incl;
-    __syncthreads();
+    rs_barrier();
     int pos = emitted + incl - cnt, total = 0;
 #pragma unroll
     for (int j = 0; j < RS_NT / 64; ++j) {
       if (j < w) pos += s_wsum[j];
       total += s_wsum[j];
     }
+    // The page lookups of the pass, then its codes, then every scale load, then the
+    // stores: each load waits only for what it depends on (the block-table row is
+    // read through its own address space, so the lookups issue together).
+    int code[RS_PER], blk[RS_PER], page[RS_PER];
+#pragma unroll
+    for (int k = 0; k < RS_PER; ++k) {
+      blk[k] = v[k] / a.cmp_block_size;
+      if (!((keep >> k) & 1u) || blk[k] >= a.cmp_table_len) blk[k] = -1;
+    }
+    if (cbt_lds) {
+#pragma unroll
+      for (int k = 0; k < RS_PER; ++k) page[k] = blk[k] >= 0 ? s_cbt[blk[k]] : -1;
+    } else {
+#pragma unroll
+      for (int k = 0; k < RS_PER; ++k) page[k] = blk[k] >= 0 ? cbt_g[blk[k]] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < RS_PER; ++k)
+      code[k] = (page[k] < 0 || page[k] >= a.cmp_block_num)
+                    ? -1
+                    : page[k] * a.cmp_block_size + (v[k] - blk[k] * a.cmp_block_size);
+    float sc[RS_PER];
+    if (sout) {
+#pragma unroll
+      for (int k = 0; k < RS_PER; ++k) sc[k] = code[k] >= 0 ? cmp_scale[code[k]] : 1.f;
+    }
 #pragma unroll
     for (int k = 0; k < RS_PER; ++k)
       if ((keep >> k) & 1u) {
-        const int code = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, v[k]);
-        out[pos] = code;
-        if (sout) put_scale(pos, code, cmp_scale);
-        aout[pos++] = code_addr(code, cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
+        out[pos] = code[k];
+        if (sout) {
+          sout[pos] = sc[k];
+          sout[inv_off + pos] = sc[k] != 0.f ? 1.f / sc[k] : 0.f;
+        }
+        aout[pos++] = code_addr(code[k], cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
       }
     emitted += total;
     if (term < limit) break;  // the list ended in this pass
-    __syncthreads();          // s_wmin / s_wsum are rewritten by the next pass
+    rs_barrier();          // s_wmin / s_wsum are rewritten by the next pass
   }
   if (tid == 0) ncmp_out[t] = emitted;
 }
