@@ -273,20 +273,26 @@ def test_bsnd_layout_with_ragged_cu_seqlens():
     assert_parity(out, lse, ref, ref_lse, label="bsnd", exact=(ex, ex_lse))
 
 
-def test_padded_page_strides():
+@pytest.mark.parametrize("kv", ["bf16", "fp8e4m3"])
+def test_padded_page_strides(kv):
     """Paged pools with padded block and row strides, as the Ascend stride-padded
     layout has (perf_compare.py:220-247): the kernel addresses rows through the
-    strides, without a repacking copy."""
-    c = make_case(B=2, H=32, seq_kv=[5000, 1300], q_per_seq=2, scenario=3, K=512, seed=14)
+    strides, without a repacking copy (fp8 rows too: their scales stay dense)."""
+    c = make_case(B=2, H=32, seq_kv=[5000, 1300], q_per_seq=2, scenario=3, K=512, seed=14,
+                  kv_dtype=kv)
     _banner("strides", c)
     d = to_device(c)
 
     def padded(pool):
-        nb, bs, _, D = pool.shape
-        base = torch.full((nb, bs + 3, 1, D + 64), float("nan"), dtype=pool.dtype, device=pool.device)
+        # NaN padding (0x7f as e4m3): a read of it would poison the output
+        fp8 = pool.dtype == torch.float8_e4m3fn
+        raw = pool.view(torch.uint8) if fp8 else pool
+        nb, bs, _, D = raw.shape
+        base = torch.full((nb, bs + 3, 1, D + 64), 0x7F if fp8 else float("nan"), dtype=raw.dtype,
+                          device=raw.device)
         view = base[:, :bs, :, :D]
-        view.copy_(pool)
-        return view
+        view.copy_(raw)
+        return view.view(torch.float8_e4m3fn) if fp8 else view
 
     d["ori_kv"] = padded(d["ori_kv"])
     d["cmp_kv"] = padded(d["cmp_kv"])
@@ -391,8 +397,8 @@ def test_device_plan_keeps_uniform_decode_unsplit():
 
 
 # ---- hipGraph capture (reference test_graph_mode.py:107-209) ----
-@pytest.mark.parametrize("with_plan", [False, True])
-def test_graph_replays_match_eager(with_plan):
+@pytest.mark.parametrize("with_plan,kv", [(False, "bf16"), (True, "bf16"), (True, "fp8e4m3")])
+def test_graph_replays_match_eager(with_plan, kv):
     """The captured forward (planner inside the graph or a plan passed in; many
     split tokens, so the combine pass is in the graph too) replayed several times,
     with other eager work and host syncs between the replays: every replay equals
@@ -402,7 +408,7 @@ def test_graph_replays_match_eager(with_plan):
     from dsv4_planb_amd.graph import SasGraph
 
     c = make_case(B=3, H=64, seq_kv=[20000, 3000, 9000], q_per_seq=[2, 1, 3], scenario=3, K=1024,
-                  seed=21)
+                  seed=21, kv_dtype=kv)
     _banner(f"graph plan={with_plan}", c)
     d = to_device(c)
     cu = d["cu_seqlens_q"]
@@ -417,7 +423,8 @@ def test_graph_replays_match_eager(with_plan):
         cmp_kv=d["cmp_kv"], cmp_block_table=d["cmp_block_table"],
         cmp_indices=d["cmp_sparse_indices"], q_prefix=cu[:-1], act_q_lens=cu[1:] - cu[:-1],
         seqused_kv=d["seqused_kv"], sinks=d["sinks"], metadata=plan, scenario=3, topk=c.K,
-        cmp_ratio=4, ori_win_left=127, softmax_scale=c.softmax_scale, core_num=1024)
+        cmp_ratio=4, ori_win_left=127, softmax_scale=c.softmax_scale, core_num=1024,
+        ori_kv_scale=d.get("ori_kv_scale"), cmp_kv_scale=d.get("cmp_kv_scale"))
     launch.run()
     torch.cuda.synchronize()
     ref_out, ref_lse = out.clone(), lse.clone()
