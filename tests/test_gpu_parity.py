@@ -191,7 +191,17 @@ def _resolution_case(kind):
     return c
 
 
-@pytest.mark.parametrize("kind", ["k300", "k4100"])
+def _resolution_case_wide_table():
+    # compressed pages of one row: block-table rows of 5000 and 7500 entries, longer
+    # than the 4096 the resolver stages in LDS, so its lookups read the table in place
+    c = make_case(B=2, H=16, seq_kv=[20000, 30000], q_per_seq=[1, 2], scenario=3, K=2048,
+                  cmp_block_size=1, seed=15)
+    c.idx[1, 7] = -1
+    c.cmp_block_table[1, 100] = -1  # an unused compressed page: its row reads as zeros
+    return c
+
+
+@pytest.mark.parametrize("kind", ["k300", "k4100", "wide_table"])
 def test_resolution_bit_exact(kind):
     """Window and compressed row codes (paged pool rows, -1 = zero row) and the
     compressed counts equal the oracle's resolution exactly."""
@@ -199,7 +209,7 @@ def test_resolution_bit_exact(kind):
     from dsv4_planb_amd import _lib
     from dsv4_planb_amd.api import build_launch
 
-    c = _resolution_case(kind)
+    c = _resolution_case_wide_table() if kind == "wide_table" else _resolution_case(kind)
     _banner("resolve-" + kind, c)
     d = to_device(c)
     launch, out, lse = build_launch(
@@ -220,9 +230,10 @@ def test_resolution_bit_exact(kind):
     torch.cuda.synchronize()
     rows, cnt = rows.cpu().numpy(), cnt.cpu().numpy()
     ref, n_ori, n_cmp = golden_c.resolve(
-        T=c.T, ori_block_table=c.ori_block_table, ori_block_size=64, q_prefix=c.q_prefix,
-        act_q=c.act_q, seqused_kv=c.seqused_kv, scenario=3, cmp_block_table=c.cmp_block_table,
-        cmp_block_size=64, cmp_sparse_indices=c.idx)
+        T=c.T, ori_block_table=c.ori_block_table, ori_block_size=c.ori_kv.shape[1],
+        q_prefix=c.q_prefix, act_q=c.act_q, seqused_kv=c.seqused_kv, scenario=3,
+        cmp_block_table=c.cmp_block_table, cmp_block_size=c.cmp_kv.shape[1],
+        cmp_sparse_indices=c.idx)
     for t in range(c.T):
         no, nc = int(n_ori[t]), int(n_cmp[t])
         assert cnt[t] == nc, (t, cnt[t], nc)
