@@ -81,6 +81,16 @@ __device__ TokInfo token_info(const SasPlanArgs& a, const int* __restrict__ q_pr
 
 constexpr int PLAN_NT = 1024;
 
+// Workgroup of the unit emitted k-th: within each full group of 16, emission order
+// 2j and 2j + 1 go to workgroups j and j + 8 (one XCD); the last partial group keeps
+// its order.  A bijection on [0, U).
+__device__ __forceinline__ int xcd_pair_slot(int k, int U) {
+  const int base = k & ~15;
+  if (base + 16 > U) return k;
+  const int r = k & 15;
+  return base + (r >> 1) + 8 * (r & 1);
+}
+
 __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
                                                        const int* __restrict__ q_prefix,
                                                        const int* __restrict__ act_q,
@@ -149,6 +159,7 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
   }
   const int U = scan_u[PLAN_NT - 1];
   int ub = scan_u[tid] - my_u, sb = scan_s[tid] - my_s, kb = scan_k[tid] - my_k;
+  const bool pair_xcd = (long long)a.T <= 4 * (long long)a.B;
   for (int t = t0; t < t1; ++t) {
     int* r = tok + (size_t)t * SAS_TOK_W;
     const int b = r[TK_B];
@@ -159,8 +170,12 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     long long ct = rows;
     if (splits > 1) ct = ((rows + splits - 1) / splits + SAS_TILE - 1) / SAS_TILE * SAS_TILE;
     for (int i = 0; i < splits; ++i) {
-      // units are emitted in reverse order so the longest (latest prefill) tokens start first
-      int* ur = units + (size_t)(U - 1 - (ub + i)) * SAS_UNIT_W;
+      // units are emitted in reverse order so the longest (latest prefill) tokens start
+      // first.  Decode-like plans (at most 4 query tokens per sequence) also put pairs of
+      // neighbouring units 8 workgroups apart: workgroups go to the 8 XCDs in turn, so
+      // the MTP tokens of a sequence, which share their window rows, share an XCD's L2.
+      const int k = U - 1 - (ub + i);
+      int* ur = units + (size_t)(pair_xcd ? xcd_pair_slot(k, U) : k) * SAS_UNIT_W;
       long long r0 = (long long)i * ct, r1 = r0 + ct < rows ? r0 + ct : rows;
       ur[0] = t;
       ur[1] = (int)r0;
