@@ -193,6 +193,8 @@ int sas_validate(const sas_params_t* p) {
       p->ori_block_stride < (int64_t)p->ori_block_size * p->ori_row_stride)
     return SAS_ERR_SHAPE;
   if ((p->ori_row_stride * es) % 16 != 0 || (p->ori_block_stride * es) % 16 != 0) return SAS_ERR_SHAPE;
+  // row codes (page * block_size + offset) are int32
+  if ((int64_t)p->ori_block_num * p->ori_block_size >= (int64_t)1 << 31) return SAS_ERR_SHAPE;
   if (p->scenario >= 2) {
     if (p->cmp_ratio < 1) return SAS_ERR_SCENARIO;
     if (p->cmp_block_num < 1 || p->cmp_block_size < 1 || p->cmp_table_len < 1) return SAS_ERR_SHAPE;

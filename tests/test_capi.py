@@ -52,6 +52,18 @@ def test_validation_codes(field, value, code):
     assert lib.sas_strerror(code).decode() not in ("", "unknown error")
 
 
+@pytest.mark.parametrize("pool", ["ori", "cmp"])
+def test_row_codes_fit_int32(pool):
+    # A row code is page * block_size + offset in int32: a pool of 2^31 rows is
+    # rejected, one row fewer is accepted.
+    lib = _lib.load()
+    kw = {f"{pool}_block_size": 2, f"{pool}_block_stride": 2 * 576}
+    ok = _good(**kw, **{f"{pool}_block_num": (1 << 30) - 1})
+    assert lib.sas_validate(ctypes.byref(ok)) == 0
+    big = _good(**kw, **{f"{pool}_block_num": 1 << 30})
+    assert lib.sas_validate(ctypes.byref(big)) == -2
+
+
 def test_sizes_and_plan_never_1024():
     lib = _lib.load()
     p = _good()
