@@ -106,7 +106,7 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
   const int per = (a.T + PLAN_NT - 1) / PLAN_NT;
   const int t0 = min(a.T, tid * per), t1 = min(a.T, t0 + per);
 
-  long long my_rows = 0;
+  long long my_rows = 0, my_longest = 0;
   for (int t = t0; t < t1; ++t) {
     TokInfo ti = token_info(a, q_prefix, act_q, seqused_kv, t);
     int* r = tok + (size_t)t * SAS_TOK_W;
@@ -116,18 +116,53 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     r[TK_NWIN] = ti.nwin;
     r[TK_WINLO] = ti.winlo;
     r[TK_NCMPMAX] = ti.ncmpmax;
-    if (ti.b >= 0) my_rows += ti.nwin + ti.ncmpmax;
+    if (ti.b >= 0) {
+      my_rows += ti.nwin + ti.ncmpmax;
+      my_longest = max(my_longest, (long long)ti.nwin + ti.ncmpmax);
+    }
   }
-  red[tid] = my_rows;
-  __syncthreads();
-  for (int off = PLAN_NT / 2; off > 0; off >>= 1) {
-    if (tid < off) red[tid] += red[tid + off];
+  // Block-wide sum (max_op: maximum); every thread gets the result.
+  auto block_reduce = [&](long long v, bool max_op) -> long long {
+    __syncthreads();  // earlier readers of red[0] are done
+    red[tid] = v;
     __syncthreads();
-  }
-  const long long R = red[0];
+    for (int off = PLAN_NT / 2; off > 0; off >>= 1) {
+      if (tid < off) red[tid] = max_op ? max(red[tid], red[tid + off]) : red[tid] + red[tid + off];
+      __syncthreads();
+    }
+    return red[0];
+  };
+  const long long R = block_reduce(my_rows, false);
   long long chunk = (R + a.target - 1) / a.target;
   if (chunk < SAS_MIN_CHUNK) chunk = SAS_MIN_CHUNK;
   chunk = (chunk + SAS_TILE - 1) / SAS_TILE * SAS_TILE;
+  // Fewer tokens than target units: the smallest chunk (a multiple of the tile) whose
+  // units number at most `target`, so that every unit starts in the first wave of
+  // workgroups.  R / target alone leaves a second, partial wave of units after the
+  // first, which doubles the time of the CUs that run one, and it splits more
+  // tokens (each split unit writes a partial the combine pass reads back).
+  if (a.T < a.target) {
+    auto units_at = [&](long long c) {
+      long long n = 0;
+      for (int t = t0; t < t1; ++t) {
+        const int* r = tok + (size_t)t * SAS_TOK_W;
+        const long long rows = r[TK_B] >= 0 ? (long long)r[TK_NWIN] + r[TK_NCMPMAX] : 0;
+        n += rows > c ? (rows + c - 1) / c : 1;
+      }
+      return n;
+    };
+    const long long longest = block_reduce(my_longest, true);
+    long long lo = chunk;  // [lo, hi]: multiples of the tile; hi gives one unit per token
+    long long hi = max(lo, (longest + SAS_TILE - 1) / SAS_TILE * SAS_TILE);
+    while (lo < hi) {
+      const long long mid = max(lo, (lo + hi) / 2 / SAS_TILE * SAS_TILE);
+      if (block_reduce(units_at(mid), false) <= a.target)
+        hi = mid;
+      else
+        lo = mid + SAS_TILE;
+    }
+    chunk = lo;
+  }
 
   int my_u = 0, my_s = 0, my_k = 0;
   for (int t = t0; t < t1; ++t) {

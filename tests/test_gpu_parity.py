@@ -381,7 +381,7 @@ def test_device_plan_covers_every_row_once(cores):
     assert (used == 1).all(), "split workspace slots overlap or go unused"
 
 
-def _plan_units(q_lens, kv, K, cores):
+def _plan_units(q_lens, kv, K, cores, with_plan=False):
     from dsv4_planb_amd import metadata as M
 
     B = len(q_lens)
@@ -396,6 +396,8 @@ def _plan_units(q_lens, kv, K, cores):
     p = plan.cpu().numpy()
     T, U, unit_cap = int(cu[-1]), int(p[3]), int(p[11])
     units = p[M.PLAN_HDR + M.PLAN_TOK_W * T:][:M.PLAN_UNIT_W * unit_cap].reshape(unit_cap, M.PLAN_UNIT_W)[:U]
+    if with_plan:
+        return units, p
     return units
 
 
@@ -405,6 +407,32 @@ def test_device_plan_keeps_uniform_decode_unsplit():
     print("\n[case] plan: uniform B=128 x 131072, 2 tokens", flush=True)
     units = _plan_units([2] * 128, [131072] * 128, 2048, 256)
     assert len(units) == 256 and (units[:, 3] == 0).all()
+
+
+def test_device_plan_fills_one_wave():
+    """A ragged batch with fewer tokens than CUs (64 sequences, KV lengths
+    log-uniform in [256, 131072], 1, 2 or 4 query tokens) gets the smallest chunk
+    whose units fit in one wave over the 256 CUs: at most 256 units, none longer
+    than the chunk, and one tile less would need more than 256."""
+    from dsv4_planb_amd import metadata as M
+
+    rng = np.random.default_rng(0)
+    kv = np.exp(rng.uniform(np.log(256), np.log(131072), size=64)).astype(np.int64).tolist()
+    q_lens = rng.choice([1, 2, 4], size=64).tolist()
+    print(f"\n[case] plan: ragged B=64, T={sum(q_lens)}", flush=True)
+    units, p = _plan_units(q_lens, kv, 2048, 256, with_plan=True)
+    T, chunk = sum(q_lens), int(p[4])
+    tok = p[M.PLAN_HDR:M.PLAN_HDR + M.PLAN_TOK_W * T].reshape(T, M.PLAN_TOK_W)
+    rows = (tok[:, 3] + tok[:, 5]).astype(np.int64)
+    assert chunk % 32 == 0 and len(units) <= 256
+    assert ((units[:, 2] - units[:, 1]) <= chunk).all()
+    n_less = sum(-(-r // (chunk - 32)) if r > chunk - 32 else 1 for r in rows)
+    assert n_less > 256, (chunk, n_less)
+    # the units of every token cover its rows once, in order
+    for t in range(T):
+        u = units[units[:, 0] == t]
+        u = u[np.argsort(u[:, 1])]
+        assert u[0, 1] == 0 and u[-1, 2] == rows[t] and (u[1:, 1] == u[:-1, 2]).all()
 
 
 # ---- hipGraph capture (reference test_graph_mode.py:107-209) ----
