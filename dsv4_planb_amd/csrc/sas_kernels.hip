@@ -255,22 +255,25 @@ __device__ __attribute__((aligned(16))) uint8_t g_zero_row[1152] = {};
 __device__ __forceinline__ uint64_t code_addr(int code, const uint8_t* pool, int block_size,
                                               int64_t block_stride, int64_t row_stride, int esz) {
   if (code < 0) return (uint64_t)g_zero_row;
-  const int page = code / block_size, off = code - page * block_size;
+  const int page = (int)((unsigned)code / (unsigned)block_size), off = code - page * block_size;
   return (uint64_t)(pool + ((size_t)page * block_stride + (size_t)off * row_stride) * esz);
 }
 
 __device__ __forceinline__ int paged_code(const int* __restrict__ bt_row, int table_len,
                                           int block_size, int block_num, int pos) {
-  const int blk = pos / block_size;
+  const int blk = (int)((unsigned)pos / (unsigned)block_size);  // pos >= 0
   const int page = blk < table_len ? bt_row[blk] : -1;
   return (page < 0 || page >= block_num) ? -1 : page * block_size + (pos - blk * block_size);
 }
 
-// One workgroup (256 threads) per token.  Thread i owns index slots
-// [RS_PER i, RS_PER (i + 1)) of the first min(K, thr) slots; the first -1 (a
-// block-wide minimum) ends the list, ids outside [0, thr) are skipped, and the
-// survivors keep their slot order through a block-wide exclusive scan.
+// One workgroup (256 threads) per token.  The first min(K, thr) index slots are
+// taken in passes of RS_PER slabs of RS_NT slots; thread i owns slot i of every
+// slab, so each load and store instruction of a wave covers 64 consecutive slots.
+// The first -1 (a block-wide minimum) ends the list, ids outside [0, thr) are
+// skipped, and the survivors keep their slot order: a wave ranks its survivors of
+// a slab with one ballot, and the per-(slab, wave) counts go through LDS.
 constexpr int RS_NT = 256;
+constexpr int RS_WAVES = RS_NT / 64;
 
 // Workgroup barrier for the resolver: its threads exchange data only through LDS,
 // so it waits for LDS operations alone.  (__syncthreads() would also drain every
@@ -278,7 +281,7 @@ constexpr int RS_NT = 256;
 __device__ __forceinline__ void rs_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
-constexpr int RS_PER = 8;  // index slots per thread and chunk
+constexpr int RS_PER = 8;  // slabs per pass (index slots per thread and pass)
 
 constexpr int RS_CBT_LDS = 4096;  // compressed block-table entries staged in LDS
 
@@ -295,35 +298,26 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
                                                         const float* __restrict__ ori_scale,
                                                         const float* __restrict__ cmp_scale,
                                                         float* __restrict__ scale_out) {
-  __shared__ int s_wmin[RS_NT / 64];
-  __shared__ int s_wsum[RS_NT / 64];
+  __shared__ int s_wmin[RS_WAVES];
+  __shared__ int s_cnt[RS_PER][RS_WAVES];
   __shared__ int s_cbt[RS_CBT_LDS];
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int* ir = idx + (size_t)t * a.K;
-  const bool vec = (a.K & 3) == 0;  // index rows are 16-B aligned
-  // Index slots [s0, s0 + RS_PER) below `bound`, all loaded before any is used
-  // (-2: past the bound).
-  auto load_slots = [&](int (&v)[RS_PER], int s0, int bound) {
-    if (vec && s0 + RS_PER <= bound) {
+  // This thread's slot of every slab of the pass at c0, all loaded before any is
+  // used (-2: at or past the bound).
+  auto load_slots = [&](int (&v)[RS_PER], int c0, int bound) {
 #pragma unroll
-      for (int k = 0; k < RS_PER; k += 4) {
-        const int4 x = *reinterpret_cast<const int4*>(ir + s0 + k);
-        v[k] = x.x;
-        v[k + 1] = x.y;
-        v[k + 2] = x.z;
-        v[k + 3] = x.w;
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < RS_PER; ++k) v[k] = s0 + k < bound ? ir[s0 + k] : -2;
+    for (int k = 0; k < RS_PER; ++k) {
+      const int sl = c0 + k * RS_NT + tid;
+      v[k] = sl < bound ? ir[sl] : -2;
     }
   };
   // First memory round trip: the token's plan record and, independent of it, the
   // first pass of its index slots.
   int v0[RS_PER];
-  if (a.scenario == 3) load_slots(v0, tid * RS_PER, a.K);
+  if (a.scenario == 3) load_slots(v0, 0, a.K);
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
   const int b = tk[TK_B];
   if (b < 0) {
@@ -378,54 +372,58 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     return;
   }
   const int limit = max(min(a.K, thr), 0);  // golden.py:48
-  // Passes of RS_NT * RS_PER slots; thread tid owns slots [RS_PER tid, RS_PER (tid + 1))
-  // of a pass; the terminator, the survivors and their slot-order positions come
-  // from block-wide reductions over registers.
+  // Passes of RS_PER slabs of RS_NT slots; the terminator, the survivors and their
+  // slot-order positions come from ballots and two LDS exchanges per pass.
   int emitted = 0;  // compressed rows written so far (block-uniform)
+  const uint64_t below = (1ull << lane) - 1;  // lanes ranked before this one
   for (int c0 = 0; c0 < limit; c0 += RS_NT * RS_PER) {
-    const int s0 = c0 + tid * RS_PER;
     int v[RS_PER];
     if (c0 == 0) {
 #pragma unroll
-      for (int k = 0; k < RS_PER; ++k) v[k] = s0 + k < limit ? v0[k] : -2;
+      for (int k = 0; k < RS_PER; ++k) v[k] = k * RS_NT + tid < limit ? v0[k] : -2;
     } else {
-      load_slots(v, s0, limit);
+      load_slots(v, c0, limit);
     }
-    // golden.py:52-53: the first -1 terminates the list
+    // golden.py:52-53: the first -1 terminates the list.  Slab k precedes slab
+    // k + 1, and within a slab wave w's 64 slots precede wave w + 1's, so a wave's
+    // first -1 is the lowest lane of its first slab that has one.
     int first = limit;
 #pragma unroll
-    for (int k = RS_PER - 1; k >= 0; --k)
-      if (v[k] == -1) first = s0 + k;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) first = min(first, __shfl_xor(first, off));
+    for (int k = RS_PER - 1; k >= 0; --k) {
+      const uint64_t m = __ballot(v[k] == -1);
+      if (m) first = c0 + k * RS_NT + w * 64 + (int)__builtin_ctzll(m);
+    }
     if (lane == 0) s_wmin[w] = first;
     rs_barrier();
     int term = s_wmin[0];
 #pragma unroll
-    for (int j = 1; j < RS_NT / 64; ++j) term = min(term, s_wmin[j]);
-    // golden.py:58-59: ids at or beyond thr are skipped (other negatives too)
-    int cnt = 0;
-    unsigned keep = 0;
+    for (int j = 1; j < RS_WAVES; ++j) term = min(term, s_wmin[j]);
+    // golden.py:58-59: ids at or beyond thr are skipped (other negatives too).
+    // Survivors of slab k are ranked within the wave by a ballot; the counts of
+    // every (slab, wave) give each wave's base position.
+    bool keep[RS_PER];
+    int rank[RS_PER];
 #pragma unroll
-    for (int k = 0; k < RS_PER; ++k)
-      if (s0 + k < term && v[k] >= 0 && v[k] < thr) {
-        keep |= 1u << k;
-        ++cnt;
-      }
-    // block-wide exclusive scan of cnt: survivors keep their slot order
-    int incl = cnt;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int x = __shfl_up(incl, off);
-      if (lane >= off) incl += x;
+    for (int k = 0; k < RS_PER; ++k) {
+      keep[k] = c0 + k * RS_NT + tid < term && v[k] >= 0 && v[k] < thr;
+      const uint64_t m = __ballot(keep[k]);
+      rank[k] = __popcll(m & below);
+      if (lane == 0) s_cnt[k][w] = __popcll(m);
     }
-    if (lane == 63) s_wsum[w] = incl;
     rs_barrier();
-    int pos = emitted + incl - cnt, total = 0;
+    int pos[RS_PER];
+    int total = emitted;
 #pragma unroll
-    for (int j = 0; j < RS_NT / 64; ++j) {
-      if (j < w) pos += s_wsum[j];
-      total += s_wsum[j];
+    for (int k = 0; k < RS_PER; ++k) {
+      int before = 0, slab = 0;
+#pragma unroll
+      for (int j = 0; j < RS_WAVES; ++j) {
+        const int c = s_cnt[k][j];
+        before += j < w ? c : 0;
+        slab += c;
+      }
+      pos[k] = total + before + rank[k];
+      total += slab;
     }
     // The page lookups of the pass, then its codes, then every scale load, then the
     // stores: each load waits only for what it depends on (the block-table row is
@@ -433,8 +431,8 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     int code[RS_PER], blk[RS_PER], page[RS_PER];
 #pragma unroll
     for (int k = 0; k < RS_PER; ++k) {
-      blk[k] = v[k] / a.cmp_block_size;
-      if (!((keep >> k) & 1u) || blk[k] >= a.cmp_table_len) blk[k] = -1;
+      blk[k] = keep[k] ? (int)((unsigned)v[k] / (unsigned)a.cmp_block_size) : -1;
+      if (blk[k] >= a.cmp_table_len) blk[k] = -1;
     }
     if (cbt_lds) {
 #pragma unroll
@@ -455,17 +453,17 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     }
 #pragma unroll
     for (int k = 0; k < RS_PER; ++k)
-      if ((keep >> k) & 1u) {
-        out[pos] = code[k];
+      if (keep[k]) {
+        out[pos[k]] = code[k];
         if (sout) {
-          sout[pos] = sc[k];
-          sout[inv_off + pos] = sc[k] != 0.f ? 1.f / sc[k] : 0.f;
+          sout[pos[k]] = sc[k];
+          sout[inv_off + pos[k]] = sc[k] != 0.f ? 1.f / sc[k] : 0.f;
         }
-        aout[pos++] = code_addr(code[k], cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
+        aout[pos[k]] = code_addr(code[k], cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
       }
-    emitted += total;
+    emitted = total;
     if (term < limit) break;  // the list ended in this pass
-    rs_barrier();          // s_wmin / s_wsum are rewritten by the next pass
+    rs_barrier();          // s_wmin / s_cnt are rewritten by the next pass
   }
   if (tid == 0) ncmp_out[t] = emitted;
 }
