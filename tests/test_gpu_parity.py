@@ -178,9 +178,16 @@ def _resolution_case(kind):
         c.idx[2, 1] = -1
         c.idx[4, 0] = 99_999
         c.ori_block_table[1, 3] = -1  # an unused page inside the window reads as zeros
+        # The resolver takes slots in slabs of 256 (64 per wave): a -1 in a later wave of
+        # slab 0 precedes one in the first wave of slab 1, and a skipped id at the end of
+        # slab 0 sits before a terminator in slab 1.
+        c.idx[7, 200] = -1
+        c.idx[7, 257] = -1
+        c.idx[8, 255] = 1_000_000
+        c.idx[8, 290] = -1
         return c
-    # K = 4100: more slots than one pass of the resolver takes (2048), vector loads,
-    # a partial last pass; a terminator and skipped ids past the first pass
+    # K = 4100: more slots than one pass of the resolver takes (2048), a partial last
+    # pass; a terminator and skipped ids past the first pass
     c = make_case(B=3, H=16, seq_kv=[20000, 30000, 17000], q_per_seq=[1, 2, 1], scenario=3,
                   K=4100, seed=13)
     c.idx[0, 3000] = -1
