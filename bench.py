@@ -519,7 +519,7 @@ def main():
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build measures one GPU only: the operator is a "
+        print(json.dumps({"error": "the benchmark measures one GPU only: the operator is a "
                           "per-GPU kernel and sharding is data-parallel over sequences "
                           "(no exchange); run with --gpus 1"}))
         sys.exit(2)

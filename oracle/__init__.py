@@ -1,6 +1,6 @@
 """Oracle for the sparse shared-KV attention path -- TEST INFRASTRUCTURE ONLY.
 
-Everything under ``oracle/`` is the checker, never the product:
+Everything under ``oracle/`` checks the product and is never part of it:
 
 * ``golden_ref``   -- numpy restatement of the reference golden model
   (``sparse_attn_sharedkv_tilelang/golden.py``): index resolution, paging,

@@ -47,7 +47,7 @@ def test_matches_reference_tables(case):
 
 # ---------------------------------------------------------------------------
 # The reference's own invariants (test_sparse_attn_sharedkv.py:767-970), run on
-# the table this build produces for every fixture argument set.
+# the table sas_metadata_legacy produces for every fixture argument set.
 # ---------------------------------------------------------------------------
 AIC, FA_W = 36, 8
 OK_CASES = [c for c in CASES if "error" not in c and c["args"].get("aic_core_num", 24) <= AIC]
