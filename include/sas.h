@@ -68,8 +68,8 @@ typedef struct {
   int32_t num_heads_kv;      /* N2: must be 1 */
   int32_t head_dim_qk;       /* 512 or 576 */
   int32_t head_dim_v;        /* 512 (<= head_dim_qk) */
-  int32_t ori_block_num, ori_block_size, ori_table_len;
-  int32_t cmp_block_num, cmp_block_size, cmp_table_len;
+  int32_t ori_block_num, ori_block_size, ori_table_len;  /* block_num * block_size < 2^31 */
+  int32_t cmp_block_num, cmp_block_size, cmp_table_len;  /* (row codes are int32)          */
   int64_t ori_block_stride;  /* elements between pages of ori_kv (>= block_size*row_stride) */
   int64_t ori_row_stride;    /* elements between rows of a page (>= head_dim_qk) */
   int64_t cmp_block_stride, cmp_row_stride;
