@@ -17,8 +17,14 @@ window 128, compression ratio 4, d_qk 576, d_v 512, scale 1/sqrt(576)):
 
 A step is one forward call (row resolution, attention, split combine) with the
 split-KV plan built beforehand by the metadata op, replayed from a hipGraph.
-``value`` is microseconds per call (lower is better).  ``roofline`` rates the
-attention kernel alone, timed with HIP events on the stream it runs on.
+``value`` is microseconds per call (lower is better), timed over exactly
+``--steps`` replays after ``--warmup`` untimed ones.  Before those, each workload
+runs ``--settle`` seconds (default 0.25) of back-to-back replays, reported as
+``settle``: the GPU clock ramps up over the first milliseconds of load (the first
+20 replays from a cold start are reported one by one as ``cold_call_us``), and a
+short warmup would otherwise time the ramp.  ``call_dist_us`` / ``attend_dist_us``
+give the per-call distribution.  ``roofline`` rates the attention kernel alone,
+timed with HIP events on the stream it runs on.
 ``cpu_baseline`` times the C oracle on a bounded sample of the same workload on
 the host cores and scales it to the full call.
 """
@@ -198,7 +204,46 @@ def _events_time(fn, n, stream):
     return start.elapsed_time(end) * 1000.0 / n  # us per call
 
 
-def measure(wl, steps, warmup, core_num=256):
+def _per_call(fn, n, stream):
+    """Each of n calls bracketed by its own events: the per-call distribution (us)."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n)]
+    for a, b in evs:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    evs[-1][1].synchronize()
+    return [a.elapsed_time(b) * 1000.0 for a, b in evs]
+
+
+def _dist(xs):
+    v = np.sort(np.asarray(xs, np.float64))
+    return {"n": int(v.size), "min": round(float(v[0]), 2), "p10": round(float(np.percentile(v, 10)), 2),
+            "median": round(float(np.median(v)), 2), "p90": round(float(np.percentile(v, 90)), 2),
+            "max": round(float(v[-1]), 2)}
+
+
+def _settle(fn, secs, stream):
+    """Back-to-back calls for `secs` seconds (host-synchronised every 32 calls so
+    the queue stays short): the GPU's clock and power reach their steady state
+    under this load before anything is timed.  Returns the number of calls."""
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < secs:
+        for _ in range(32):
+            fn()
+        n += 32
+        stream.synchronize()
+    return n
+
+
+def measure(wl, steps, warmup, core_num=256, settle_s=0.25):
+    """Per workload: build the plan and launch, capture the forward call in a
+    hipGraph, then (1) the first 20 replays timed one by one from a cold start
+    (`cold_call_us`: the clock ramp), (2) a settle phase of `settle_s` seconds of
+    back-to-back replays, (3) `warmup` untimed replays, (4) the timed region:
+    exactly `steps` replays between two events (`call_us`, the headline), (5) the
+    per-call distribution of `steps` more replays, (6) each stage alone and the
+    eager API call."""
     from dsv4_planb_amd import sparse_attn_sharedkv
     from dsv4_planb_amd.graph import SasGraph
 
@@ -211,18 +256,22 @@ def measure(wl, steps, warmup, core_num=256):
         torch.cuda.synchronize()
         plan_host_us = (time.perf_counter() - t0) * 1e6  # metadata op + launch set-up
         cu = wl["cu"]
-        for _ in range(max(warmup, 1)):
-            launch.run()
+        launch.run()
         torch.cuda.synchronize()
         graph = SasGraph(launch)
-        for _ in range(max(warmup, 1)):
-            graph.replay(stream)
+        replay = lambda: graph.replay(stream)  # noqa: E731
+        cold = _per_call(replay, 20, stream)
+        settle_calls = _settle(replay, settle_s, stream)
+        for _ in range(warmup):
+            replay()
         torch.cuda.synchronize()
         # the timed region: `steps` full forward calls replayed from the graph
-        call_us = _events_time(lambda: graph.replay(stream), steps, stream)
+        call_us = _events_time(replay, steps, stream)
         torch.cuda.synchronize()
+        call_dist = _dist(_per_call(replay, max(steps, 10), stream))
         # the stages alone (same stream, same inputs)
         attend_us = _events_time(lambda: launch.run("attend"), steps, stream)
+        attend_dist = _dist(_per_call(lambda: launch.run("attend"), max(steps, 10), stream))
         resolve_us = _events_time(lambda: launch.run("resolve"), steps, stream)
         combine_us = _events_time(lambda: launch.run("combine"), steps, stream)
         plan_p = launch.params
@@ -246,7 +295,9 @@ def measure(wl, steps, warmup, core_num=256):
     ok = bool(torch.isfinite(out.float()).all().item())
     return dict(call_us=call_us, attend_us=attend_us, resolve_us=resolve_us,
                 combine_us=combine_us, plan_us=plan_us, plan_host_us=plan_host_us,
-                eager_api_us=eager_us, finite=ok)
+                eager_api_us=eager_us, finite=ok, call_dist_us=call_dist,
+                attend_dist_us=attend_dist, cold_call_us=[round(x, 1) for x in cold],
+                settle={"seconds": settle_s, "calls": settle_calls})
 
 
 def _traffic_from_profile(workload):
@@ -498,6 +549,9 @@ def main():
                     choices=["decode128k", "prefill8k", "decode32", "decode128k_fp8", "ragged_fp8"])
     ap.add_argument("--extra", default="prefill8k,decode32,decode128k_fp8,ragged_fp8",
                     help="comma-separated extra workloads reported under 'workloads' ('' = none)")
+    ap.add_argument("--settle", type=float, default=0.25,
+                    help="seconds of back-to-back calls per workload before its warmup and timed "
+                         "region (the clock and power reach steady state); reported as 'settle'")
     ap.add_argument("--cpu-seqs", type=int, default=0,
                     help="cap on sampled sequences for the CPU baseline (0 = size for ~10 s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -545,7 +599,7 @@ def main():
         _log(f"{name}: building inputs")
         wl = make_workload(name, seed=0, dev=dev)
         _log(f"{name}: timing")
-        r = measure(wl, args.steps, args.warmup)
+        r = measure(wl, args.steps, args.warmup, settle_s=args.settle)
         _log(f"{name}: call {r['call_us']:.1f} us, attend {r['attend_us']:.1f} us")
         attend_s = r["attend_us"] * 1e-6
         r.update(alg_bytes=wl["alg_bytes"], alg_flops=wl["alg_flops"], uniq_rows=wl["uniq_rows"],

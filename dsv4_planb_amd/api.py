@@ -15,10 +15,14 @@ Differences from the reference, all extensions:
   scales ``ori_kv_scale`` / ``cmp_kv_scale`` ``[block_num, block_size, 1]``.
 * paged KV may carry padded block / row strides (the reference benchmark's
   stride-padded layout, ``sparse_attn_sharedkv_perf_compare.py:220-247``).
-* ``metadata`` may be the reference's int32[1024] table (accepted and
-  validated; the GPU builds its own split-KV plan for all CUs) or a plan from
+* ``metadata`` may be the reference's int32[1024] table or a plan from
   :func:`dsv4_planb_amd.metadata.sparse_attn_sharedkv_metadata` with
-  ``aic_core_num > 36``.
+  ``aic_core_num > 36``.  The 1024-entry table partitions query rows over the
+  reference's 24-36 cores; the partition does not change any result, so the
+  table is accepted by its size and the GPU builds its own split-KV plan for all
+  CUs in the same stream (the planner kernel).  A plan is checked on the device
+  against the call's arguments: a mismatch zeroes the outputs and sets the
+  workspace status word (:meth:`SasLaunch.device_status`).
 * No host synchronisation happens when every tensor is already on the device,
   so the call can be captured into a graph.
 """
@@ -89,6 +93,12 @@ class SasLaunch:
         self.plan = plan
         self.ws = ws
         self.device = device
+
+    def device_status(self) -> int:
+        """The workspace status word of the last forward call: 0, or -8
+        (``SAS_ERR_PLAN``) when the plan passed in was built for other arguments
+        and the outputs were zeroed.  Synchronises the device."""
+        return int(self.ws[:4].view(torch.int32).item())
 
     def run(self, stage: str = "forward"):
         lib = _lib.load()

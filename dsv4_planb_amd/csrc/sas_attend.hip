@@ -38,10 +38,11 @@
 // bf16-rounded P that enter PV, so O / l_w is exactly a convex combination of
 // the V rows (a one-hot softmax returns its row unchanged, as the reference's
 // P = 1 does); l_e sums the unrounded P and gives the LSE.  A logit more than
-// REDO_SLACK above the frame (where 2^SLACK times the row count nears the fp32
-// range) makes the workgroup discard the pass and recompute the unit framed on
-// the maximum each head observed (a second, separately inlined copy of the unit
-// body, so the common path carries no extra live state).
+// redo_slack() above the frame (64 for bf16 queries, 15 for fp16, whose largest
+// finite value is below 2^16; with fp8 KV and fp16 queries also a rounded P s
+// above 2^15) makes the workgroup discard the pass and recompute the unit framed
+// on the maximum each head observed (a second, separately inlined copy of the
+// unit body, so the common path carries no extra live state).
 //
 // LDS tile = latent region (32 rows x 512 dims at a 1088-B row stride, i.e. 64 B
 // of padding per row) + rope region (32 rows x 64 dims, 128-B rows; absent at
@@ -75,7 +76,12 @@
 
 namespace sas {
 
-constexpr float REDO_SLACK = 64.f;
+// How far (log2 units) a logit may rise above the unit's frame before the unit is
+// redone in a frame set on the observed maximum: P = 2^(x - m) enters PV rounded
+// to the query dtype, so 2^SLACK must stay finite there (bf16: 2^64, far inside its
+// range, with 2^64 times the row count far inside fp32's; fp16: 2^15 <= 65504).
+template <int QT>
+constexpr float redo_slack() { return QT == 0 ? 64.f : 15.f; }
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -221,10 +227,10 @@ __device__ __forceinline__ bool attend_unit(
   }
 
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
-  const int nwin = tk[TK_NWIN];
+  const int nwin = min(tk[TK_NWIN], a.win_left + 1);
   const int splits = tk[TK_SPLITS], wsbase = tk[TK_WSBASE];
   const int r0 = ur[1];
-  const int r1 = min(ur[2], nwin + ncmp[t]);
+  const int r1 = min(min(ur[2], nwin + ncmp[t]), a.list_stride);
   const int ntiles = r1 > r0 ? (r1 - r0 + TILE - 1) / TILE : 0;
   // row addresses of this unit's list (pool addresses; -1 codes read the zero row)
   const uint64_t* alist = addr_list + (size_t)t * a.list_stride + r0;
@@ -307,6 +313,7 @@ __device__ __forceinline__ bool attend_unit(
       if (lse && g == 0) lse[(size_t)t * H + h] = (sink2 + __log2f(l_sink)) * 0.6931471805599453f;
     } else {
       const int slot = wsbase + split;
+      if (slot < 0 || slot >= a.slot_cap) return false;  // (a sound plan never gets here)
       float* orow = ws_o + ((size_t)slot * H + h) * DV + 16 * g;
 #pragma unroll
       for (int mb = 0; mb < 16; ++mb)
@@ -610,6 +617,7 @@ __device__ __forceinline__ bool attend_unit(
   // ---- softmax of one tile: P = 2^(S c - m) rounded to bf16, sums ----
   float pe = 0.f;          // sum of P (LSE), per lane
   float pw = 0.f;          // sum of bf16(P): what entered PV (output normaliser)
+  float pmax = 0.f;        // fp16 q with fp8 KV: the largest P s rounded for PV
   float xo = -INFINITY;    // max of x - m over the unit, for the overflow guard
   const float c = a.scale_log2;
   // The max over the tile of both half-waves (lane l and lane l ^ 32 hold the two
@@ -656,11 +664,17 @@ __device__ __forceinline__ bool attend_unit(
       x1 = __builtin_amdgcn_exp2f(x1);
       asm volatile("" : "+v"(x0), "+v"(x1));
     } else if (ph == 2) {
-      uint32_t p = KV8 ? pack2_q16<QT>(x0 * sc[0], x1 * sc[1]) : pack2_q16<QT>(x0, x1);
+      const float y0 = KV8 ? x0 * sc[0] : x0, y1 = KV8 ? x1 * sc[1] : x1;
+      uint32_t p = pack2_q16<QT>(y0, y1);
       float e = pe + (x0 + x1);
       asm volatile("" : "+v"(p), "+v"(e));
       pk[k >> 2][k & 3] = p;
       pe = e;
+      if constexpr (KV8 && QT == 1) {  // the scale can push P s past fp16's range
+        float pm = fmaxf(pmax, fmaxf(y0, y1));
+        asm volatile("" : "+v"(pm));
+        pmax = pm;
+      }
     } else if constexpr (KV8) {
       const uint32_t p = pk[k >> 2][k & 3];
       float w2 = fmaf(q16_to_f32<QT>(p >> 16), iv[1], fmaf(q16_to_f32<QT>(p & 0xffffu), iv[0], pw));
@@ -887,7 +901,9 @@ __device__ __forceinline__ bool attend_unit(
 
   // ---- overflow guard: a logit far above the frame redoes the whole unit ----
   if (!REDO) {
-    if (__any(xobs > REDO_SLACK) && lane == 0) atomicOr(&sm.far, 1);
+    bool over = xobs > redo_slack<QT>();
+    if constexpr (KV8 && QT == 1) over = over || pmax > 32768.f;  // 2^15, as the slack
+    if (__any(over) && lane == 0) atomicOr(&sm.far, 1);
     lds_barrier();
     if (sm.far) {
       m_obs = m_run + xobs;
@@ -936,6 +952,7 @@ __device__ __forceinline__ bool attend_unit(
     if (lse && g == 0) lse[(size_t)t * H + h] = (m_run + __log2f(l_e)) * 0.6931471805599453f;
   } else {  // an un-normalised partial (O, m, l_w, l_e) for the combine pass
     const int slot = wsbase + split;
+    if (slot < 0 || slot >= a.slot_cap) return false;  // (a sound plan never gets here)
     // registers 4 qd .. 4 qd + 3 of block mb: d = 32 mb + 16 g + 4 qd .. (16-bit KV),
     // 32 mb + 8 qd + 4 g .. (fp8)
     float* orow = ws_o + ((size_t)slot * H + h) * DV + (KV8 ? 4 : 16) * g;
@@ -970,7 +987,16 @@ __global__ __launch_bounds__(256, 1) void attend_kernel(
     float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   __shared__ __attribute__((aligned(16))) AttendLds<DQK, KV8> sm;
   const int u = blockIdx.x;
-  if (plan[PH_MAGIC] != SAS_PLAN_MAGIC || u >= plan[PH_UNITS]) return;
+  if (!plan_matches(plan, a)) {  // a plan built for other arguments: zeros (the resolver
+    if (u < a.T) {               // flagged the call in the workspace status word)
+      for (int i = threadIdx.x; i < a.H * 512 / 8; i += 256)
+        reinterpret_cast<u32x4_t*>(out + (size_t)u * a.H * 512)[i] = u32x4_t{0, 0, 0, 0};
+      if (lse)
+        for (int i = threadIdx.x; i < a.H; i += 256) lse[(size_t)u * a.H + i] = 0.f;
+    }
+    return;
+  }
+  if (u >= plan[PH_UNITS]) return;
   float m_obs = 0.f;
   if (attend_unit<DQK, QT, STREAM, KV8, false>(u, sm, a, q, addr_list, scale_list, ncmp, sinks, plan,
                                                out, lse, ws_o, ws_ml, m_obs)) {

@@ -63,6 +63,7 @@ SasFwdArgs fwd_args(const sas_params_t* p, int target) {
   a.list_stride = (int)sas_row_list_stride(p->ori_win_left, a.K, p->scenario);
   a.unit_cap = (int)sas_plan_layout(p->total_tokens, target).unit_cap;
   a.split_cap = target;
+  a.slot_cap = 2 * target;
   return a;
 }
 
@@ -96,6 +97,7 @@ int check_tensors(const sas_params_t* p, const sas_tensors_t* t) {
 }
 
 struct Ws {
+  int* status;
   int* rows;
   uint64_t* addr;
   float* scale;  // fp8 KV only
@@ -112,6 +114,7 @@ int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out)
   if (!ws || ws_bytes < W.total) return SAS_ERR_WORKSPACE;
   if (((uintptr_t)ws & 255u) != 0) return SAS_ERR_WORKSPACE;
   char* base = static_cast<char*>(ws);
+  out->status = reinterpret_cast<int*>(base + W.off_status);
   out->rows = reinterpret_cast<int*>(base + W.off_rows);
   out->addr = reinterpret_cast<uint64_t*>(base + W.off_addr);
   out->scale = p->kv_dtype == SAS_DT_FP8E4M3 ? reinterpret_cast<float*>(base + W.off_scale) : nullptr;
@@ -163,7 +166,7 @@ const char* sas_strerror(int code) {
     case SAS_ERR_MASK_MODE: return "only ori_mask_mode=4, cmp_mask_mode=3, ori_win_right=0 supported";
     case SAS_ERR_HEADS: return "num_heads_kv must be 1 and num_heads_q in [1, 128]";
     case SAS_ERR_WORKSPACE: return "workspace missing, misaligned or too small";
-    case SAS_ERR_PLAN: return "plan buffer too small";
+    case SAS_ERR_PLAN: return "plan buffer too small, or a plan built for other arguments";
     case SAS_ERR_LAUNCH: return "HIP kernel launch failed";
     case SAS_ERR_METADATA: return "invalid metadata arguments";
     case SAS_ERR_GRAPH: return "hipGraph capture or instantiation failed";
@@ -260,7 +263,7 @@ int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   if (!plan) plan = w.plan;
   if (p->total_tokens == 0) return SAS_OK;
   hipLaunchKernelGGL(sas::resolve_kernel, dim3(p->total_tokens), dim3(sas::RS_NT), 0,
-                     (hipStream_t)stream, fwd_args(p, target), plan, t->ori_block_table,
+                     (hipStream_t)stream, fwd_args(p, target), plan, w.status, t->ori_block_table,
                      t->cmp_sparse_indices, t->cmp_block_table, w.rows, w.ncmp, w.addr,
                      static_cast<const uint8_t*>(t->ori_kv), static_cast<const uint8_t*>(t->cmp_kv),
                      p->kv_dtype == SAS_DT_FP8E4M3 ? 1 : 2, t->ori_kv_scale, t->cmp_kv_scale, w.scale);

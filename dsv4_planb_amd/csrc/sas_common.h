@@ -15,12 +15,17 @@
 // ---- split-KV plan (int32 buffer written by the planner kernel) ----
 // header
 #define SAS_PLAN_MAGIC 0x53415350  // 'SASP'
-#define SAS_PLAN_VERSION 1
-#define SAS_PLAN_HDR 16
+#define SAS_PLAN_VERSION 2
+#define SAS_PLAN_HDR 24
+// PH_T .. PH_CMP_RATIO record the arguments the plan was built for; the kernels
+// refuse a plan whose record differs from the call's (plan_matches below).
+// PH_STATUS holds the planner's own invariant checks (PS_* bits, 0 = sound).
 enum {
   PH_MAGIC = 0, PH_VERSION, PH_T, PH_UNITS, PH_CHUNK, PH_TARGET, PH_NSPLIT_TOKENS,
-  PH_NSLOTS, PH_TOTAL_ROWS_LO, PH_TOTAL_ROWS_HI, PH_H, PH_UNIT_CAP, PH_SCENARIO, PH_K
+  PH_NSLOTS, PH_TOTAL_ROWS_LO, PH_TOTAL_ROWS_HI, PH_H, PH_UNIT_CAP, PH_SCENARIO, PH_K,
+  PH_WIN_LEFT, PH_B, PH_CMP_RATIO, PH_STATUS
 };
+enum { PS_UNITS_OVER_CAP = 1, PS_SLOTS_OVER_CAP = 2, PS_SPLIT_TOKENS_OVER_CAP = 4 };
 // per-token record [T][8]
 #define SAS_TOK_W 8
 enum { TK_B = 0, TK_S, TK_SG, TK_NWIN, TK_WINLO, TK_NCMPMAX, TK_SPLITS, TK_WSBASE };
@@ -53,8 +58,11 @@ SAS_HD static inline SasPlanLayout sas_plan_layout(int64_t T, int64_t target) {
 }
 
 // ---- workspace (bytes, each region 256-B aligned) ----
+// The first int32 of the workspace is the status word of the last forward call on
+// it: 0, or SAS_ERR_PLAN when the plan did not match the call (the outputs are then
+// zeros).  The resolver writes it on every call.
 struct SasWsLayout {
-  size_t off_rows, off_addr, off_scale, off_ncmp, off_plan, off_o, off_ml, total;
+  size_t off_status, off_rows, off_addr, off_scale, off_ncmp, off_plan, off_o, off_ml, total;
   int64_t slot_cap;
 };
 
@@ -72,6 +80,8 @@ SAS_HD static inline SasWsLayout sas_ws_layout(int64_t T, int64_t K, int64_t H, 
                                         bool kv8) {
   SasWsLayout W;
   size_t off = 0;
+  W.off_status = off;
+  off = sas_align256(off + 4);
   W.off_rows = off;
   off = sas_align256(off + (size_t)(T > 0 ? T : 1) * sas_row_list_stride(win_left, K, scenario) * 4);
   // 64-bit row addresses, same shape as the code lists, plus one tile of slack
@@ -112,5 +122,21 @@ struct SasFwdArgs {
   int32_t cmp_block_size, cmp_table_len, cmp_block_num;
   int64_t ori_block_stride, ori_row_stride, cmp_block_stride, cmp_row_stride;  // elements
   float scale_log2;  // softmax_scale * log2(e)
-  int32_t unit_cap, split_cap;
+  int32_t unit_cap, split_cap;  // plan capacities (split_cap = target units)
+  int32_t slot_cap;             // split partial slots in the workspace (2 * target)
 };
+
+// Does the plan describe this call?  Magic and version, the token and batch
+// counts, the scenario, the window, the ratio (scenarios 2 and 3), the balance
+// target (which sizes the plan and the partial slots) and, in scenario 3, the
+// index slots per token; and the planner's own invariants held.  (Scenario 2
+// plans may bound the compressed list differently: the resolver caps it at the
+// call's K, and each token's row count is min(K, thr) either way.)
+SAS_HD static inline bool plan_matches(const int* plan, const SasFwdArgs& a) {
+  return plan[PH_MAGIC] == SAS_PLAN_MAGIC && plan[PH_VERSION] == SAS_PLAN_VERSION &&
+         plan[PH_T] == a.T && plan[PH_B] == a.B && plan[PH_SCENARIO] == a.scenario &&
+         plan[PH_WIN_LEFT] == a.win_left &&
+         (a.scenario == 1 || plan[PH_CMP_RATIO] == a.cmp_ratio) &&
+         plan[PH_TARGET] == a.split_cap && (a.scenario != 3 || plan[PH_K] == a.K) &&
+         plan[PH_STATUS] == 0;
+}

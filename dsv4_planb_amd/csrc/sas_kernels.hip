@@ -210,7 +210,9 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
       // neighbouring units 8 workgroups apart: workgroups go to the 8 XCDs in turn, so
       // the MTP tokens of a sequence, which share their window rows, share an XCD's L2.
       const int k = U - 1 - (ub + i);
-      int* ur = units + (size_t)(pair_xcd ? xcd_pair_slot(k, U) : k) * SAS_UNIT_W;
+      const int slot = pair_xcd ? xcd_pair_slot(k, U) : k;
+      if (slot < 0 || slot >= L.unit_cap) continue;  // (U <= unit_cap: flagged below if not)
+      int* ur = units + (size_t)slot * SAS_UNIT_W;
       long long r0 = (long long)i * ct, r1 = r0 + ct < rows ? r0 + ct : rows;
       ur[0] = t;
       ur[1] = (int)r0;
@@ -219,7 +221,8 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     }
     ub += splits;
     if (splits > 1) {
-      stoks[kb++] = t;
+      if (kb < L.split_cap) stoks[kb] = t;
+      ++kb;
       sb += splits;
     }
   }
@@ -238,6 +241,19 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     plan[PH_UNIT_CAP] = (int)L.unit_cap;
     plan[PH_SCENARIO] = a.scenario;
     plan[PH_K] = a.K;
+    plan[PH_WIN_LEFT] = a.win_left;
+    plan[PH_B] = a.B;
+    plan[PH_CMP_RATIO] = a.cmp_ratio;
+    // The capacities hold by construction (split tokens have more rows than the
+    // chunk >= R / target, so fewer than `target` of them exist, with at most
+    // 2 * target units; every token has at most rows / chunk + 1 units); a plan
+    // that broke one is refused by every kernel.
+    int status = 0;
+    if ((long long)U > L.unit_cap) status |= PS_UNITS_OVER_CAP;
+    if ((long long)scan_s[PLAN_NT - 1] > 2 * (long long)a.target) status |= PS_SLOTS_OVER_CAP;
+    if ((long long)scan_k[PLAN_NT - 1] > L.split_cap) status |= PS_SPLIT_TOKENS_OVER_CAP;
+    plan[PH_STATUS] = status;
+    for (int i = PH_STATUS + 1; i < SAS_PLAN_HDR; ++i) plan[i] = 0;
   }
 }
 
@@ -286,6 +302,7 @@ constexpr int RS_PER = 8;  // slabs per pass (index slots per thread and pass)
 constexpr int RS_CBT_LDS = 4096;  // compressed block-table entries staged in LDS
 
 __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int* __restrict__ plan,
+                                                        int* __restrict__ status,
                                                         const int* __restrict__ ori_bt,
                                                         const int* __restrict__ idx,
                                                         const int* __restrict__ cmp_bt,
@@ -318,9 +335,13 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
   // first pass of its index slots.
   int v0[RS_PER];
   if (a.scenario == 3) load_slots(v0, 0, a.K);
+  // A plan built for other arguments is refused: the call's status word says so,
+  // every token resolves to no rows, and the attention kernel writes zeros.
+  const bool plan_ok = plan_matches(plan, a);
+  if (t == 0 && tid == 0) *status = plan_ok ? SAS_OK : SAS_ERR_PLAN;
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
-  const int b = tk[TK_B];
-  if (b < 0) {
+  const int b = plan_ok ? tk[TK_B] : -1;
+  if (b < 0 || b >= a.B) {
     if (tid == 0) ncmp_out[t] = 0;
     return;
   }
@@ -336,7 +357,7 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     sout[r] = s;
     sout[inv_off + r] = s != 0.f ? 1.f / s : 0.f;
   };
-  const int nwin = tk[TK_NWIN], winlo = tk[TK_WINLO];
+  const int nwin = min(tk[TK_NWIN], a.win_left + 1), winlo = tk[TK_WINLO];
   // Second: the window's block-table entries and the batch's compressed block-table
   // row, staged in LDS so the per-id page lookups below stay on chip.
   const int* cbt_g = cmp_bt + (size_t)b * a.cmp_table_len;
@@ -609,6 +630,7 @@ __global__ __launch_bounds__(64 * COMBINE_WAVES) void combine_kernel(
     SasFwdArgs a, const int* __restrict__ plan, const float* __restrict__ ws_o,
     const float* __restrict__ ws_ml, uint16_t* __restrict__ out, float* __restrict__ lse) {
   const int H = a.H;
+  if (!plan_matches(plan, a)) return;  // refused plan: the attention kernel wrote zeros
   const int items = plan[PH_NSPLIT_TOKENS] * H;  // (split token, head) pairs
   const SasPlanLayout L = sas_plan_layout(a.T, a.split_cap);
   const int wave = blockIdx.x * COMBINE_WAVES + (threadIdx.x >> 6);

@@ -46,7 +46,11 @@ FD_M_NUM_INDEX = 6
 
 # split-KV plan header (csrc/sas_common.h)
 PLAN_MAGIC = 0x53415350
-PLAN_HDR = 16
+PLAN_VERSION = 2
+PLAN_HDR = 24
+# header fields (csrc/sas_common.h PH_*)
+PH_T, PH_UNITS, PH_CHUNK, PH_TARGET, PH_NSPLIT_TOKENS, PH_NSLOTS = 2, 3, 4, 5, 6, 7
+PH_UNIT_CAP, PH_SCENARIO, PH_K, PH_WIN_LEFT, PH_B, PH_CMP_RATIO, PH_STATUS = 11, 12, 13, 14, 15, 16, 17
 PLAN_TOK_W = 8
 PLAN_UNIT_W = 4
 

@@ -52,7 +52,8 @@ typedef enum {
   SAS_ERR_MASK_MODE = -5,     /* mask modes / window other than the supported ones */
   SAS_ERR_HEADS = -6,         /* num_heads_kv != 1 or num_heads_q out of range */
   SAS_ERR_WORKSPACE = -7,     /* workspace too small */
-  SAS_ERR_PLAN = -8,          /* plan buffer too small or not a plan */
+  SAS_ERR_PLAN = -8,          /* plan buffer too small, or (workspace status word) a plan
+                                 built for other arguments: the outputs were zeroed */
   SAS_ERR_LAUNCH = -9,        /* HIP launch error */
   SAS_ERR_METADATA = -10,     /* legacy metadata arguments invalid */
   SAS_ERR_GRAPH = -11,        /* graph capture / instantiate failed */
@@ -125,7 +126,11 @@ int sas_plan(const sas_params_t* p, const int32_t* q_prefix, const int32_t* act_
              const int32_t* seqused_kv, int32_t* plan, size_t plan_n_int32, sas_stream_t stream);
 /* Full forward: (plan if plan == NULL) -> index resolution -> attention ->
  * split combine.  plan may be a buffer filled by sas_plan for the same params
- * and lengths. */
+ * and lengths.  The plan's header records the arguments it was built for (token
+ * and batch counts, scenario, window, ratio, top-k, balance target); the kernels
+ * refuse a plan whose record differs from the call: the outputs are written as
+ * zeros and the first int32 of the workspace (the status word, written by every
+ * call) reads SAS_ERR_PLAN instead of SAS_OK. */
 int sas_forward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
                 void* workspace, size_t workspace_bytes, sas_stream_t stream);
 /* The stages of sas_forward, for timing and debugging (same workspace).

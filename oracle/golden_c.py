@@ -59,8 +59,21 @@ def load():
     lib.sasg_resolve.argtypes = [ctypes.POINTER(SasgParams), P, P, P, P, P, P, ctypes.c_int32,
                                  P, P, P]
     lib.sasg_resolve.restype = ctypes.c_int
+    lib.sasg_round.argtypes = [ctypes.c_int, P, P, ctypes.c_int64]
+    lib.sasg_round.restype = ctypes.c_int
     _lib = lib
     return lib
+
+
+def round_array(x: np.ndarray, dtype: str) -> np.ndarray:
+    """The C oracle's rounding of float32 values to ``dtype`` ("bf16" or "fp16"),
+    returned as float32 (the step it applies to P before PV and to the output)."""
+    src = np.ascontiguousarray(x, dtype=np.float32)
+    dst = np.empty_like(src)
+    rc = load().sasg_round(DT_CODES[dtype], _ptr(src), _ptr(dst), src.size)
+    if rc != 0:
+        raise RuntimeError(f"sasg_round: {rc}")
+    return dst
 
 
 def _ptr(a: Optional[np.ndarray]):

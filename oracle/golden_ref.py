@@ -30,11 +30,19 @@ SRC_CMP = 1
 # Rounding helpers (the reference casts P and the output to q's dtype).
 # --------------------------------------------------------------------------
 def round_bf16(x: np.ndarray) -> np.ndarray:
-    """Round float32 to the nearest bfloat16 (ties to even); returns float32."""
+    """Round float32 to the nearest bfloat16 (ties to even); returns float32.
+
+    Adding 0x7FFF plus the lowest kept bit to the bit pattern and clearing the
+    low 16 bits rounds to nearest even on the magnitude, for either sign.  For
+    every non-NaN input the sum stays below 2^32 (the largest finite pattern is
+    0xFF7FFFFF), so it runs in uint32; NaNs are restored afterwards."""
     x = np.asarray(x, dtype=np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
-    out = r.view(np.float32).copy()
+    u = x.view(np.uint32)
+    r = (u >> 16) & np.uint32(1)
+    r += np.uint32(0x7FFF)
+    r += u
+    r &= np.uint32(0xFFFF0000)
+    out = r.view(np.float32)
     nan = np.isnan(x)
     if nan.any():
         out[nan] = np.nan

@@ -418,4 +418,12 @@ int sasg_attention_exact(const sasg_params* p, const void* q, const void* ori_kv
   return err;
 }
 
+/* Test hook: the oracle's own rounding of n floats to the dtype dt (SASG_BF16 or
+ * SASG_F16; other codes copy), so its rounding can be checked against a library. */
+int sasg_round(int dt, const float* x, float* y, int64_t n) {
+  if (!x || !y || n < 0) return -1;
+  for (int64_t i = 0; i < n; ++i) y[i] = round_to(x[i], dt);
+  return 0;
+}
+
 int sasg_version(void) { return 1; }

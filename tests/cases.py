@@ -152,11 +152,18 @@ def make_case(
     value_scale: float = 1.0,
     index_mode: str = "random",
     dist: str = "normal",
+    pool_pages: Optional[int] = None,
+    cmp_pool_pages: Optional[int] = None,
 ) -> Case:
     """``dist="normal"``: q and KV ~ N(0, value_scale^2) (the benchmark
     configurations).  ``dist="reference"``: the reference suite's own draws --
     q and raw KV ~ U(-10, 10), compressed KV ~ U(-5, 10)
-    (test_sparse_attn_sharedkv.py:262, golden.py:315-408)."""
+    (test_sparse_attn_sharedkv.py:262, golden.py:315-408).
+
+    ``pool_pages`` / ``cmp_pool_pages``: a shared page pool of that many pages,
+    each sequence's block table a random permutation of it (truncated to the
+    sequence's pages), so long contexts fit host memory; otherwise every
+    sequence owns its pages (one random permutation over all of them)."""
     rng = np.random.default_rng(seed)
     seq_kv = [int(x) for x in seq_kv]
     qps = [int(q_per_seq)] * B if isinstance(q_per_seq, int) else [int(x) for x in q_per_seq]
@@ -167,28 +174,35 @@ def make_case(
     def draw(shape, lo_hi):
         if dist == "reference":
             return rng.uniform(lo_hi[0], lo_hi[1], size=shape).astype(np.float32)
-        return (rng.standard_normal(shape) * value_scale).astype(np.float32)
+        x = rng.standard_normal(shape, dtype=np.float32)
+        return x if value_scale == 1.0 else x * np.float32(value_scale)
 
     q = draw((T, H, D), (-10.0, 10.0))
     q_bits = _encode(q, q_dtype)
 
-    def paged_pool(lens: List[int], bs: int, lo_hi):
+    def paged_pool(lens: List[int], bs: int, lo_hi, shared: Optional[int]):
         per = [math.ceil(n / bs) if n > 0 else 0 for n in lens]
-        nb = sum(per) + extra_pages
-        perm = rng.permutation(nb).astype(np.int32)
         table = np.full((B, max(max(per), 1)), -1, np.int32)
-        cur = 0
-        for b, n in enumerate(per):
-            table[b, :n] = perm[cur:cur + n]
-            cur += n
+        if shared is not None:
+            assert max(per) <= shared, "a sequence needs more pages than the shared pool holds"
+            nb = shared
+            for b, n in enumerate(per):
+                table[b, :n] = rng.permutation(nb)[:n].astype(np.int32)
+        else:
+            nb = sum(per) + extra_pages
+            perm = rng.permutation(nb).astype(np.int32)
+            cur = 0
+            for b, n in enumerate(per):
+                table[b, :n] = perm[cur:cur + n]
+                cur += n
         vals = draw((nb, bs, D), lo_hi)
         return vals, table
 
-    ori_vals, ori_bt = paged_pool(seq_kv, block_size, (-10.0, 10.0))
+    ori_vals, ori_bt = paged_pool(seq_kv, block_size, (-10.0, 10.0), pool_pages)
     cmp_vals = cmp_bt = None
     if scenario >= 2:
         cmp_vals, cmp_bt = paged_pool([n // cmp_ratio for n in seq_kv], cmp_block_size,
-                                      (-5.0, 10.0))
+                                      (-5.0, 10.0), cmp_pool_pages)
 
     ori_scale = cmp_scale = None
     if kv_dtype == "fp8e4m3":

@@ -84,3 +84,57 @@ def test_null_arguments_rejected_without_launch():
     assert lib.sas_forward(ctypes.byref(p), ctypes.byref(t), None, None, 0, None) == -1
     assert lib.sas_plan(ctypes.byref(p), None, None, None, None, 0, None) == -1
     assert lib.sas_graph_launch(None, None) == -1
+
+
+COMMON = os.path.join(os.path.dirname(os.path.dirname(__file__)), "dsv4_planb_amd", "csrc",
+                      "sas_common.h")
+
+
+def test_plan_header_mirror_matches_c_header():
+    """The Python mirror of the plan header (dsv4_planb_amd.metadata) agrees with
+    csrc/sas_common.h: field positions, header size, version and magic."""
+    from dsv4_planb_amd import metadata as M
+
+    txt = open(COMMON).read()
+    body = re.search(r"enum \{\s*(PH_MAGIC = 0,[^}]*)\}", txt).group(1)
+    fields = [f.strip() for f in body.replace("\n", " ").split(",") if f.strip()]
+    pos = {name.split("=")[0].strip(): i for i, name in enumerate(fields)}
+    for name in ("PH_T", "PH_UNITS", "PH_CHUNK", "PH_TARGET", "PH_NSPLIT_TOKENS", "PH_NSLOTS",
+                 "PH_UNIT_CAP", "PH_SCENARIO", "PH_K", "PH_WIN_LEFT", "PH_B", "PH_CMP_RATIO",
+                 "PH_STATUS"):
+        assert getattr(M, name) == pos[name], name
+    assert len(fields) <= M.PLAN_HDR
+    assert int(re.search(r"#define SAS_PLAN_HDR (\d+)", txt).group(1)) == M.PLAN_HDR
+    assert int(re.search(r"#define SAS_PLAN_VERSION (\d+)", txt).group(1)) == M.PLAN_VERSION
+    assert int(re.search(r"#define SAS_PLAN_MAGIC (0x[0-9A-Fa-f]+)", txt).group(1), 16) == M.PLAN_MAGIC
+
+
+@pytest.mark.parametrize("T,cores", [(1, 256), (256, 256), (8192, 256), (6, 1024)])
+def test_plan_and_workspace_sizes(T, cores):
+    """Plan: header, 8 ints per token, 4 per unit (capacity T + target), one per
+    possible split token (target).  Workspace: a 256-B status word region first,
+    then the row lists of every token (window + top-k slots), their addresses,
+    the counts, a copy of the plan and 2 * target partial slots."""
+    from dsv4_planb_amd import metadata as M
+
+    lib = _lib.load()
+    p = _good(total_tokens=T, num_cus=cores, topk=2048, num_heads_q=128)
+    n = ctypes.c_size_t()
+    assert lib.sas_plan_size(ctypes.byref(p), ctypes.byref(n)) == 0
+    expect = M.PLAN_HDR + M.PLAN_TOK_W * T + M.PLAN_UNIT_W * (T + cores) + cores
+    assert n.value == (expect + 1 if expect == 1024 else expect)
+    ws = ctypes.c_size_t()
+    assert lib.sas_workspace_size(ctypes.byref(p), ctypes.byref(ws)) == 0
+
+    def al(x):
+        return (x + 255) // 256 * 256
+
+    stride = 128 + 2048
+    expect_ws = (al(4) + al(T * stride * 4) + al((T * stride + 32) * 8) + al(T * 4) + al(n.value * 4)
+                 + al(2 * cores * 128 * 512 * 4) + al(2 * cores * 128 * 16))
+    assert ws.value == expect_ws
+
+
+def test_plan_status_strings():
+    lib = _lib.load()
+    assert "other arguments" in lib.sas_strerror(-8).decode()

@@ -1,0 +1,107 @@
+"""GPU parity on the code paths the benchmark's headline workloads run.
+
+* 128 sequences x 131072 KV, 2 query tokens each, 128 heads, top-k 2048, 256
+  CUs: the plan gives every token one 2176-row unit (68 tiles), the gather is
+  non-temporal, the two tokens of a sequence share an XCD, and nothing is split
+  (no combine).  The block tables are per-sequence random permutations of a
+  shared page pool (4096 raw pages, 1024 compressed pages) so the inputs fit in
+  host memory; the kernels address rows the same way whatever pool they sit in.
+* One sequence of 8192 query tokens over 8192 KV, 128 heads, top-k 2048 over the
+  causally valid compressed rows: 8192 one-token units of 1..2176 rows with the
+  cached gather.  The oracle checks a stratified subset of 512 tokens (all of
+  the output is computed), which covers tokens with 1 to 2048 compressed rows.
+
+Both compare every checked token with the C oracle and with the float64 exact
+value (tests/gpu_helpers.assert_parity).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from tests.cases import make_case
+from tests.gpu_helpers import assert_parity, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def _plan(c, d, cores=256):
+    from dsv4_planb_amd import metadata as M
+
+    plan = M.sparse_attn_sharedkv_metadata(
+        num_heads_q=c.H, num_heads_kv=1, head_dim=c.D, cu_seqlens_q=d["cu_seqlens_q"],
+        seqused_kv=d["seqused_kv"], batch_size=c.B, max_seqlen_q=int(c.act_q.max()),
+        max_seqlen_kv=int(c.seqused_kv.max()), cmp_topk=c.K, cmp_ratio=c.cmp_ratio,
+        layout_q="TND", has_cmp_kv=True, aic_core_num=cores)
+    torch.cuda.synchronize()
+    return plan
+
+
+def _units(M, p, T):
+    U, unit_cap = int(p[M.PH_UNITS]), int(p[M.PH_UNIT_CAP])
+    base = M.PLAN_HDR + M.PLAN_TOK_W * T
+    return p[base:base + M.PLAN_UNIT_W * unit_cap].reshape(unit_cap, M.PLAN_UNIT_W)[:U]
+
+
+def _run_and_check(name, c, plan, tokens=None):
+    from dsv4_planb_amd import sparse_attn_sharedkv
+
+    d = to_device(c)
+    q = d.pop("q")
+    out, lse = sparse_attn_sharedkv(q, softmax_scale=c.softmax_scale, cmp_ratio=c.cmp_ratio,
+                                    ori_win_left=c.win_left, layout_q="TND",
+                                    return_softmax_lse=True, topk_cmp=c.K, metadata=plan,
+                                    core_num=256, **d)
+    torch.cuda.synchronize()
+    if tokens is not None:
+        sel = torch.as_tensor(np.asarray(tokens), device=out.device)
+        out, lse = out.index_select(0, sel), lse.index_select(0, sel)
+    out = out.float().cpu().numpy()
+    lse = lse.cpu().numpy()
+    print(f"[{name}] device done; oracle ...", flush=True)
+    ref, ref_lse = c.oracle_c(tokens=tokens)
+    ex, ex_lse = c.oracle_exact(tokens=tokens)
+    if tokens is not None:
+        ref, ref_lse, ex, ex_lse = ref[tokens], ref_lse[tokens], ex[tokens], ex_lse[tokens]
+    return assert_parity(out, lse, ref, ref_lse, dtype=c.q_dtype, label=name, exact=(ex, ex_lse))
+
+
+def test_decode128k_full_batch_one_unit_per_token():
+    from dsv4_planb_amd import metadata as M
+
+    print("\n[case] decode128k full: B=128 T=256 H=128 K=2048 KV=131072 (shared pools)", flush=True)
+    c = make_case(B=128, H=128, seq_kv=[131072] * 128, q_per_seq=2, scenario=3, K=2048, seed=31,
+                  pool_pages=4096, cmp_pool_pages=1024)
+    d = to_device(c)
+    plan = _plan(c, d)
+    p = plan.cpu().numpy()
+    units = _units(M, p, c.T)
+    # the benchmark's plan: one 2176-row unit per token, no split tokens
+    assert int(p[M.PH_UNITS]) == c.T == 256 and int(p[M.PH_NSPLIT_TOKENS]) == 0
+    assert int(p[M.PH_CHUNK]) == 2176
+    assert (units[:, 3] == 0).all() and ((units[:, 2] - units[:, 1]) == 2176).all()
+    assert sorted(units[:, 0].tolist()) == list(range(c.T))
+    del d
+    _run_and_check("decode128k[full]", c, plan)
+
+
+def test_prefill8k_full_size_stratified_tokens():
+    from dsv4_planb_amd import metadata as M
+
+    print("\n[case] prefill8k full: B=1 T=8192 H=128 K=2048 KV=8192", flush=True)
+    c = make_case(B=1, H=128, seq_kv=[8192], q_per_seq=8192, scenario=3, K=2048, seed=41)
+    d = to_device(c)
+    plan = _plan(c, d)
+    p = plan.cpu().numpy()
+    units = _units(M, p, c.T)
+    assert int(p[M.PH_UNITS]) == c.T and int(p[M.PH_NSPLIT_TOKENS]) == 0
+    assert (units[:, 3] == 0).all()
+    del d
+    # 512 tokens spread over the sequence, plus the first and the last: compressed
+    # row counts (t + 1) // 4 from 0 (the first tokens) to 2048 (the last token)
+    tokens = sorted(set(np.linspace(0, c.T - 1, 512).round().astype(int).tolist()) | {0, c.T - 1})
+    ncmp = [min((t + 1) // 4, 2048) for t in tokens]
+    assert min(ncmp) == 0 and max(ncmp) == 2048
+    _run_and_check("prefill8k[full,512 tok]", c, plan, tokens=tokens)

@@ -34,7 +34,7 @@ def _check(name, c, tokens=None, rule="baseline", **extra):
         out, lse, ref, ref_lse = out[tokens], lse[tokens], ref[tokens], ref_lse[tokens]
         ex, ex_lse = ex[tokens], ex_lse[tokens]
     return assert_parity(out, lse, ref, ref_lse, dtype=c.q_dtype, label=name,
-                         exact=(ex, ex_lse), rule=rule)
+                         exact=(ex, ex_lse), rule=rule, kv8=c.kv_dtype == "fp8e4m3")
 
 
 # ---- benchmark configurations (full size where the oracle is quick) ----
@@ -108,25 +108,70 @@ def test_fp8_paths(name, build, extra, rule):
     _check(name, c, tokens=toks, rule=rule, **extra)
 
 
-# ---- reference scenarios (test_sparse_attn_sharedkv.py:81-220): D=512, H=64, page 128,
-# the reference's own value draws (q / raw KV ~ U(-10,10), compressed KV ~ U(-5,10));
-# prefills at S1=1024 as in test_sparse_attn_sharedkv_fast.py ----
-def _ref_case(scenario, s1, kv, ratio, K, D=512, seed=42):
+# ---- reference scenarios (test_sparse_attn_sharedkv.py:81-220): H=64, page 128, the
+# reference's own value draws (q / raw KV ~ U(-10,10), compressed KV ~ U(-5,10)) and
+# its flow: the metadata op at its default 24 cores, then the API with that table
+# (test_sparse_attn_sharedkv.py:530-629).  Decodes and the 8192-token prefills, plus
+# the S1=1024 prefills of test_sparse_attn_sharedkv_fast.py; bf16 and fp16 as the
+# reference runs them (:637), at its d=512 and at d_qk=576 (512 latent + 64 rope). ----
+def _ref_case(scenario, s1, kv, ratio, K, D=512, dtype="bf16", seed=42):
     c = make_case(B=1, H=64, D=D, seq_kv=[kv], q_per_seq=s1, scenario=scenario, K=K,
                   cmp_ratio=ratio, block_size=128, cmp_block_size=128, seed=seed,
-                  softmax_scale=0.04419417, dist="reference")
+                  softmax_scale=0.04419417, dist="reference", q_dtype=dtype, kv_dtype=dtype)
     return c
 
 
-@pytest.mark.parametrize("name,scen,s1,kv,ratio,K", [
+def _metadata24(c):
+    from dsv4_planb_amd import sparse_attn_sharedkv_metadata
+
+    kw = dict(num_heads_q=c.H, num_heads_kv=1, head_dim=c.D,
+              cu_seqlens_q=torch.from_numpy(c.cu_seqlens_q), seqused_kv=torch.from_numpy(c.seqused_kv),
+              batch_size=c.B, max_seqlen_q=int(c.act_q.max()), max_seqlen_kv=int(c.seqused_kv.max()),
+              ori_mask_mode=4, ori_win_left=127, ori_win_right=0, layout_q="TND", layout_kv="PA_ND",
+              has_ori_kv=True, has_cmp_kv=c.scenario >= 2)
+    if c.scenario >= 2:
+        kw.update(cmp_ratio=c.cmp_ratio, cmp_mask_mode=3)
+    if c.scenario == 3:
+        kw["cmp_topk"] = c.K
+    md = sparse_attn_sharedkv_metadata(**kw)
+    assert md.numel() == 1024 and md.dtype == torch.int32
+    return md.cuda()
+
+
+_REF_SCENARIOS = [
     ("scfa_decode", 3, 1, 8193, 4, 512), ("swa_decode", 1, 1, 8193, 4, 0),
-    ("cfa_decode", 2, 1, 8193, 128, 0), ("scfa_prefill_fast", 3, 1024, 1024, 4, 512),
-    ("swa_prefill_fast", 1, 1024, 1024, 4, 0), ("cfa_prefill_fast", 2, 1024, 1024, 128, 0),
-])
-def test_reference_scenarios(name, scen, s1, kv, ratio, K):
-    c = _ref_case(scen, s1, kv, ratio, K)
-    toks = None if s1 == 1 else list(range(0, s1, 5)) + [s1 - 1]
-    _check(name, c, tokens=toks, rule="reference")
+    ("cfa_decode", 2, 1, 8193, 128, 0), ("scfa_prefill", 3, 8192, 8192, 4, 512),
+    ("swa_prefill", 1, 8192, 8192, 4, 0), ("cfa_prefill", 2, 8192, 8192, 128, 0),
+    ("scfa_prefill_fast", 3, 1024, 1024, 4, 512), ("swa_prefill_fast", 1, 1024, 1024, 4, 0),
+    ("cfa_prefill_fast", 2, 1024, 1024, 128, 0),
+]
+
+
+@pytest.mark.parametrize("D", [512, 576])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("name,scen,s1,kv,ratio,K", _REF_SCENARIOS)
+def test_reference_scenarios(name, scen, s1, kv, ratio, K, dtype, D):
+    c = _ref_case(scen, s1, kv, ratio, K, D=D, dtype=dtype)
+    _check(f"{name}[{dtype},d{D}]", c, rule="reference", metadata=_metadata24(c))
+
+
+def test_fp16_short_prefill_tokens_reference_draws():
+    """fp16 queries on the reference's large-magnitude draws, prefill tokens of
+    1..100 window rows plus up to 25 compressed rows (1 to 4 tiles): later tiles
+    rise up to tens of log2 units above the first tile's maximum, so P = 2^(x - m)
+    would leave fp16's range without the fp16 redo bound."""
+    c = make_case(B=2, H=64, D=512, seq_kv=[100, 60], q_per_seq=[100, 60], scenario=3, K=64,
+                  block_size=128, cmp_block_size=128, q_dtype="fp16", kv_dtype="fp16", seed=81,
+                  softmax_scale=0.04419417, dist="reference")
+    _check("fp16_short_prefill", c, rule="reference")
+
+
+def test_fp16_query_fp8_kv_reference_draws():
+    """fp16 queries with fp8 KV on the reference's draws: the row scale enters
+    P s, which the redo bound covers as well."""
+    c = make_case(B=2, H=64, D=576, seq_kv=[100, 3000], q_per_seq=[100, 2], scenario=3, K=256,
+                  q_dtype="fp16", kv_dtype="fp8e4m3", seed=82, dist="reference")
+    _check("fp16q_fp8kv_reference", c, rule="reference_fp8")
 
 
 def test_fp16_scfa():
@@ -503,3 +548,61 @@ def test_graph_replays_match_eager(with_plan, kv):
             assert torch.equal(lse, ref2_lse), f"refreshed replay {k}: lse differs"
     finally:
         graph.close()
+
+
+# ---- plans built for other arguments are refused on the device ----
+@pytest.mark.parametrize("what", ["window", "topk", "batch", "target"])
+def test_plan_for_other_arguments_is_refused(what):
+    """A split-KV plan records the arguments it was built for.  A plan that does
+    not match the call (another window, top-k, batch split or balance target)
+    makes every kernel refuse it: the outputs are zeros and the workspace status
+    word reads SAS_ERR_PLAN.  The matching plan gives the oracle's answer and
+    status 0."""
+    from dsv4_planb_amd import metadata as M
+    from dsv4_planb_amd.api import build_launch
+
+    c = make_case(B=3, H=32, seq_kv=[5000, 1300, 9000], q_per_seq=[2, 1, 3], scenario=3, K=512,
+                  seed=91)
+    _banner(f"plan-mismatch-{what}", c)
+    d = to_device(c)
+    cu = d["cu_seqlens_q"]
+
+    def plan_for(win=127, K=c.K, cu_=cu, cores=256):
+        return M.sparse_attn_sharedkv_metadata(
+            num_heads_q=c.H, num_heads_kv=1, head_dim=c.D, cu_seqlens_q=cu_,
+            seqused_kv=d["seqused_kv"][:cu_.numel() - 1], batch_size=cu_.numel() - 1,
+            max_seqlen_q=3, max_seqlen_kv=9000, cmp_topk=K, cmp_ratio=4, ori_win_left=win,
+            layout_q="TND", has_cmp_kv=True, aic_core_num=cores)
+
+    def launch_with(plan):
+        launch, out, lse = build_launch(
+            q_flat=d["q"], ori_kv=d["ori_kv"], ori_block_table=d["ori_block_table"],
+            cmp_kv=d["cmp_kv"], cmp_block_table=d["cmp_block_table"],
+            cmp_indices=d["cmp_sparse_indices"], q_prefix=cu[:-1], act_q_lens=cu[1:] - cu[:-1],
+            seqused_kv=d["seqused_kv"], sinks=d["sinks"], metadata=plan, scenario=3, topk=c.K,
+            cmp_ratio=4, ori_win_left=127, softmax_scale=c.softmax_scale, core_num=256)
+        out.fill_(float("nan"))
+        lse.fill_(float("nan"))
+        launch.run()
+        torch.cuda.synchronize()
+        return launch, out, lse
+
+    launch, out, lse = launch_with(plan_for())
+    assert launch.device_status() == 0
+    oc, lc = c.oracle_c()
+    assert_parity(out.float().cpu().numpy(), lse.cpu().numpy(), oc, lc, label="plan-match")
+    if what == "window":
+        bad = plan_for(win=63)
+    elif what == "topk":
+        bad = plan_for(K=256)
+    elif what == "batch":  # the same 6 tokens as one sequence of 6
+        cu1 = torch.tensor([0, c.T], dtype=torch.int32, device="cuda")
+        bad = plan_for(cu_=cu1)
+    else:  # planned for 512 CUs: a different plan and partial-slot layout (padded to size)
+        bad = plan_for(cores=512)
+        n = launch.plan.numel()
+        bad = torch.cat([bad, torch.zeros(max(0, n - bad.numel()), dtype=torch.int32,
+                                          device="cuda")])[:n]
+    launch, out, lse = launch_with(bad)
+    assert launch.device_status() == -8, "SAS_ERR_PLAN expected in the workspace status word"
+    assert not out.float().abs().sum().item() and not lse.abs().sum().item(), "outputs must be zeros"

@@ -14,6 +14,7 @@ import math
 import numpy as np
 import pytest
 
+from oracle import golden_c
 from oracle import golden_ref as G
 from tests.cases import make_case
 
@@ -318,13 +319,131 @@ def test_planted_minus_one_skip_instead_of_break_is_caught():
     assert G.resolve_cmp_ids(row, act_kv=100, act_q=1, s_local=0, cmp_ratio=4) == [3]
 
 
-def test_planted_missing_p_rounding_changes_bf16_result(monkeypatch):
-    c = make_case(B=1, H=8, seq_kv=[2000], q_per_seq=1, K=600, seed=8)
-    out_ok, _ = c.oracle_numpy()
-    monkeypatch.setattr(G, "round_to", lambda x, dt: np.asarray(x, np.float32) if dt != "bf16" or x.ndim == 2 else G.round_bf16(x))
-    out_bad, _ = c.oracle_numpy()
-    # the output cast survives; only the P cast is dropped -- a visible but small change
-    assert np.abs(out_ok - out_bad).max() > 0
+# --------------------------------------------------------------------------
+# Rounding to the query dtype (P before PV, and the output), against torch.
+# --------------------------------------------------------------------------
+def _tie_patterns():
+    """Every float32 sign / exponent / kept-mantissa pattern (the high 16 bits)
+    with low halves at the bf16 rounding boundaries: exact, just above, just
+    below and exactly at the tie, and the tie +- 1 (0x8000 ties to even, with the
+    kept bit 0 or 1 as the high half gives)."""
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    lows = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32)
+    return (hi[:, None] | lows[None, :]).ravel().view(np.float32)
+
+
+def test_round_bf16_numpy_and_c_match_torch_at_every_tie_pattern():
+    import torch
+
+    x = _tie_patterns()
+    rng = np.random.default_rng(0)
+    x = np.concatenate([x, rng.standard_normal(1 << 16, dtype=np.float32) * 100])
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    nan = np.isnan(want)
+    for name, got in (("numpy", G.round_bf16(x)), ("C", golden_c.round_array(x, "bf16"))):
+        assert (np.isnan(got) == nan).all(), name
+        np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32),
+                                      err_msg=name)
+
+
+def test_round_f16_c_and_numpy_match_torch_at_every_tie():
+    """fp16: the midpoints between neighbouring finite fp16 values (ties to even),
+    the values a float32 ulp either side, the subnormal range and overflow."""
+    import torch
+
+    h = np.arange(1 << 16, dtype=np.uint16).view(np.float16)
+    fin = h[np.isfinite(h)].astype(np.float64)
+    fin = np.unique(fin)
+    mids = ((fin[1:] + fin[:-1]) / 2).astype(np.float32)  # exact in float32
+    x = np.concatenate([mids, np.nextafter(mids, np.inf), np.nextafter(mids, -np.inf),
+                        fin.astype(np.float32), np.float32([65519.0, 65520.0, -65520.0, 1e6])])
+    want = torch.from_numpy(x).to(torch.float16).to(torch.float32).numpy()
+    for name, got in (("numpy", G.round_to(x, "fp16")), ("C", golden_c.round_array(x, "fp16"))):
+        np.testing.assert_array_equal(got, want, err_msg=name)
+
+
+# --------------------------------------------------------------------------
+# The bf16 / fp16 rounding of P before PV (golden.py:194), by a closed form
+# that a dropped or a truncating rounding fails.
+# --------------------------------------------------------------------------
+def _p_rounding_case(dtype):
+    """Two keys in one window, no sink: x0 = 0 (P0 = 1) and x1 = ln p with
+    p = 1 - 2.4 u (u: the dtype's spacing just below 1), V0 = +e0 and V1 = -e0.
+    Then out[0] = (1 - r(p)) / (1 + p): r(p) = 1 - 2u rounded to nearest,
+    1 - 3u truncated, 1 - 2.4 u unrounded -- three outputs far apart.  The logit
+    sits in the rope dimension 512, which V (the first 512 columns) omits."""
+    from tests.cases import Case
+
+    u = 2.0 ** (-8 if dtype == "bf16" else -11)
+    p_target = 1.0 - 2.4 * u
+    scale = 1.0 / 24.0
+    D = 576
+    kv = np.zeros((1, 64, D), np.float32)
+    kv[0, 0, 0] = 1.0
+    kv[0, 1, 0] = -1.0
+    kv[0, 1, 512] = math.log(p_target) / scale
+    q = np.zeros((1, 1, D), np.float32)
+    q[0, 0, 512] = 1.0
+    enc = (lambda a: G.f32_to_bf16_bits(a)) if dtype == "bf16" else (
+        lambda a: a.astype(np.float16).view(np.uint16))
+    c = Case(B=1, H=1, D=D, Dv=512, T=1, scenario=1, cmp_ratio=4, win_left=127,
+             softmax_scale=scale, q_dtype=dtype, kv_dtype=dtype,
+             cu_seqlens_q=np.array([0, 1], np.int32), q_prefix=np.array([0], np.int32),
+             act_q=np.array([1], np.int32), seqused_kv=np.array([2], np.int32),
+             q_bits=enc(q), ori_kv=enc(kv), ori_block_table=np.array([[0]], np.int32),
+             sinks=np.array([-np.inf], np.float32))
+    # the stored logit and P, in float64: far (0.1 u) from any rounding boundary
+    k1 = float(c.ori_f32()[0, 1, 512])
+    p = math.exp(k1 * scale)
+    assert abs((1.0 - p) / u - 2.4) < 0.02
+    rnd = (lambda v: float(G.round_bf16(np.float32([v]))[0])) if dtype == "bf16" else (
+        lambda v: float(np.float32(v).astype(np.float16)))
+    cand = {
+        "nearest": 1.0 - 2.0 * u,
+        "truncated": 1.0 - 3.0 * u,
+        "none": p,
+    }
+    outs = {k: rnd(np.float32((np.float32(1.0) - np.float32(v)) / np.float32(1.0 + p)))
+            for k, v in cand.items()}
+    assert len(set(outs.values())) == 3, outs
+    return c, outs
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_p_rounding_to_nearest_closed_form(dtype):
+    c, outs = _p_rounding_case(dtype)
+    for name, (out, _) in (("numpy", c.oracle_numpy()), ("C", c.oracle_c())):
+        assert float(out[0, 0, 0]) == outs["nearest"], (name, float(out[0, 0, 0]), outs)
+
+
+def _plant_p_rounding(monkeypatch, mode):
+    """Replace the oracle's rounding of P (the 2-D [heads, rows] tile) only; the
+    output cast keeps the real rounding."""
+    real = G.round_to
+
+    def planted(x, dt):
+        x = np.asarray(x, np.float32)
+        if x.ndim != 2 or x.shape[1] == 512:  # not a P tile (an output row block)
+            return real(x, dt)
+        if mode == "dropped":
+            return x
+        u = x.view(np.uint32) & np.uint32(0xFFFF0000 if dt == "bf16" else 0xFFFFFFFF)
+        if dt == "bf16":
+            return u.view(np.float32)
+        return np.trunc(x * 2048.0) / 2048.0  # fp16 values in [0.5, 1): spacing 2^-11
+
+    monkeypatch.setattr(G, "round_to", planted)
+
+
+@pytest.mark.parametrize("mode", ["dropped", "truncated"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_planted_p_rounding_mistakes_are_caught(monkeypatch, dtype, mode):
+    c, outs = _p_rounding_case(dtype)
+    _plant_p_rounding(monkeypatch, mode)
+    out, _ = c.oracle_numpy()
+    got = float(out[0, 0, 0])
+    assert got != outs["nearest"]
+    assert got == outs["none" if mode == "dropped" else "truncated"]
 
 
 # --------------------------------------------------------------------------
