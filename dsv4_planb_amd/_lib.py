@@ -18,7 +18,7 @@ ERR_NAMES = {
     -1: "SAS_ERR_NULL", -2: "SAS_ERR_SHAPE", -3: "SAS_ERR_DTYPE", -4: "SAS_ERR_SCENARIO",
     -5: "SAS_ERR_MASK_MODE", -6: "SAS_ERR_HEADS", -7: "SAS_ERR_WORKSPACE", -8: "SAS_ERR_PLAN",
     -9: "SAS_ERR_LAUNCH", -10: "SAS_ERR_METADATA", -11: "SAS_ERR_GRAPH",
-    -12: "SAS_ERR_NOT_IMPLEMENTED",
+    -12: "SAS_ERR_NOT_IMPLEMENTED", -13: "SAS_ERR_SCRATCH",
 }
 DT_BF16, DT_FP16, DT_FP8E4M3 = 1, 2, 3
 SAS_META_SIZE = 1024
@@ -28,8 +28,9 @@ SYMBOLS = (
     "sas_strerror", "sas_version", "sas_validate", "sas_workspace_size", "sas_plan_size",
     "sas_target_units", "sas_plan", "sas_forward", "sas_resolve", "sas_attend", "sas_combine",
     "sas_debug_rows", "sas_graph_capture", "sas_graph_launch", "sas_graph_destroy",
-    "sas_metadata_legacy",
+    "sas_metadata_legacy", "sas_forward_noalloc",
 )
+SAS_SCRATCH_BYTES = 160 << 20  # include/sas.h: the fixed workspace of sas_forward_noalloc
 
 
 class SasParams(ctypes.Structure):
@@ -104,6 +105,7 @@ def load():
         for fn in ("sas_forward", "sas_resolve", "sas_attend", "sas_combine"):
             getattr(lib, fn).argtypes = [PP, PT, P, P, S, P]
         lib.sas_debug_rows.argtypes = [PP, P, P, P, P]
+        lib.sas_forward_noalloc.argtypes = [PP, PT, P, P]
         lib.sas_graph_capture.argtypes = [PP, PT, P, P, S, P, ctypes.POINTER(P)]
         lib.sas_graph_launch.argtypes = [P, P]
         lib.sas_graph_destroy.argtypes = [P]

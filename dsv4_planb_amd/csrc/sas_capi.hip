@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "sas_common.h"
 #include "sas_kernels.hip"
@@ -171,6 +172,9 @@ const char* sas_strerror(int code) {
     case SAS_ERR_METADATA: return "invalid metadata arguments";
     case SAS_ERR_GRAPH: return "hipGraph capture or instantiation failed";
     case SAS_ERR_NOT_IMPLEMENTED: return "not implemented";
+    case SAS_ERR_SCRATCH:
+      return "the call needs more workspace than the fixed scratch buffer of "
+             "sas_forward_noalloc (SAS_SCRATCH_BYTES); use sas_forward with a workspace";
     default: return "unknown error";
   }
 }
@@ -350,6 +354,49 @@ int sas_debug_rows(const sas_params_t* p, const void* ws, int32_t* rows, int32_t
                      hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)
     return SAS_ERR_LAUNCH;
   return SAS_OK;
+}
+
+}  // extern "C"
+
+// ---- the allocation-free variant of sas_forward ----
+// Its workspace is this fixed device array (one copy per GPU, held until the
+// process ends).  In host code `scratch` names a host-side stand-in, not device
+// memory: its device address comes from hipGetSymbolAddress, once per device with
+// that device current, and only that address is ever handed to a kernel.
+static __device__ __attribute__((aligned(256))) uint8_t scratch[SAS_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (looked up on the first call per device).
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SAS_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return SAS_ERR_LAUNCH;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SAS_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int sas_forward_noalloc(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
+                        sas_stream_t stream) {
+  void* ws = nullptr;
+  int rc = scratch_for_current_device(&ws);  // first, so that any call sets the device up
+  if (rc) return rc;
+  if ((rc = sas_validate(p))) return rc;
+  size_t need = 0;
+  if ((rc = sas_workspace_size(p, &need))) return rc;
+  if (need > (size_t)SAS_SCRATCH_BYTES) return SAS_ERR_SCRATCH;
+  return sas_forward(p, t, plan, ws, (size_t)SAS_SCRATCH_BYTES, stream);
 }
 
 int sas_graph_capture(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,

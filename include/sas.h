@@ -57,7 +57,8 @@ typedef enum {
   SAS_ERR_LAUNCH = -9,        /* HIP launch error */
   SAS_ERR_METADATA = -10,     /* legacy metadata arguments invalid */
   SAS_ERR_GRAPH = -11,        /* graph capture / instantiate failed */
-  SAS_ERR_NOT_IMPLEMENTED = -12
+  SAS_ERR_NOT_IMPLEMENTED = -12,
+  SAS_ERR_SCRATCH = -13       /* sas_forward_noalloc: the call needs more than SAS_SCRATCH_BYTES */
 } sas_status_t;
 
 typedef enum { SAS_DT_BF16 = 1, SAS_DT_FP16 = 2, SAS_DT_FP8E4M3 = 3 } sas_dtype_t;
@@ -142,6 +143,19 @@ int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pla
                void* workspace, size_t workspace_bytes, sas_stream_t stream);
 int sas_combine(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
                 void* workspace, size_t workspace_bytes, sas_stream_t stream);
+/* The allocation-free variant of sas_forward.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Instead of a
+ * caller workspace it uses a fixed device array of SAS_SCRATCH_BYTES inside the
+ * library, one per GPU, held until the process ends; a call whose workspace
+ * (sas_workspace_size) is larger returns SAS_ERR_SCRATCH.  It calls no allocator.
+ * Every call on one GPU shares that array: calls that overlap on one GPU (other
+ * streams, other threads) race.  The first call on each device looks the array's
+ * address up (hipGetSymbolAddress); make that first call outside graph capture
+ * (any call does it, even one that returns an error for its arguments). */
+#define SAS_SCRATCH_BYTES (160u << 20)
+int sas_forward_noalloc(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
+                        sas_stream_t stream);
 /* Debug: copy the resolved row-code lists of every token into rows (int32
  * [T, win_left + 1 (+ topk in scenarios 2, 3)]: the token's window pool rows, then
  * directly after them its compressed pool rows; -1 = a row read as zeros) and the

@@ -1,0 +1,90 @@
+"""sas_forward_noalloc: the forward call whose workspace is the library's fixed
+device scratch array (no allocation), through the C ABI.
+
+Two calls in a row (a split-heavy one, then a smaller one on the same GPU) must
+equal sas_forward with a caller workspace bit for bit: same plan, same kernels,
+so the same sums in the same order.  A call whose workspace would exceed the
+scratch array is refused with SAS_ERR_SCRATCH before anything is launched.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from tests.cases import make_case
+from tests.gpu_helpers import assert_parity, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def _launch(c, core_num):
+    from dsv4_planb_amd.api import build_launch
+
+    d = to_device(c)
+    cu = d["cu_seqlens_q"]
+    return build_launch(
+        q_flat=d["q"], ori_kv=d["ori_kv"], ori_block_table=d["ori_block_table"],
+        cmp_kv=d.get("cmp_kv"), cmp_block_table=d.get("cmp_block_table"),
+        cmp_indices=d.get("cmp_sparse_indices"), q_prefix=cu[:-1], act_q_lens=cu[1:] - cu[:-1],
+        seqused_kv=d["seqused_kv"], sinks=d["sinks"], metadata=None, scenario=c.scenario,
+        topk=c.K, cmp_ratio=c.cmp_ratio, ori_win_left=c.win_left, softmax_scale=c.softmax_scale,
+        core_num=core_num, ori_kv_scale=d.get("ori_kv_scale"), cmp_kv_scale=d.get("cmp_kv_scale"))
+
+
+def _noalloc(launch):
+    from dsv4_planb_amd import _lib
+
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return _lib.load().sas_forward_noalloc(ctypes.byref(launch.params), ctypes.byref(launch.tensors),
+                                          None, stream)
+
+
+def test_noalloc_matches_forward_on_two_calls():
+    from dsv4_planb_amd import _lib
+
+    cases = [
+        ("noalloc-1", make_case(B=6, H=128, seq_kv=[20000, 3000, 131072, 700, 9000, 40000],
+                                q_per_seq=[2, 1, 2, 4, 1, 2], scenario=3, K=2048, seed=101,
+                                pool_pages=2100, cmp_pool_pages=600), 256),
+        ("noalloc-2", make_case(B=2, H=64, seq_kv=[5000, 1300], q_per_seq=[1, 2], scenario=3,
+                                K=512, seed=102), 256),
+    ]
+    for name, c, cores in cases:
+        print(f"\n[case] {name}: B={c.B} T={c.T} H={c.H} K={c.K}", flush=True)
+        launch, out, lse = _launch(c, cores)
+        need = ctypes.c_size_t()
+        _lib.check(_lib.load().sas_workspace_size(ctypes.byref(launch.params), ctypes.byref(need)))
+        assert need.value <= _lib.SAS_SCRATCH_BYTES
+        launch.run()
+        torch.cuda.synchronize()
+        ref_out, ref_lse = out.clone(), lse.clone()
+        out.fill_(float("nan"))
+        lse.fill_(float("nan"))
+        torch.cuda.synchronize()
+        rc = _noalloc(launch)
+        assert rc == 0, _lib.strerror(rc)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_out), f"{name}: output differs from sas_forward"
+        assert torch.equal(lse, ref_lse), f"{name}: lse differs from sas_forward"
+        oc, lc = c.oracle_c()
+        assert_parity(out.float().cpu().numpy(), lse.cpu().numpy(), oc, lc, label=name)
+
+
+def test_noalloc_refuses_a_call_larger_than_the_scratch():
+    """8192 query tokens with top-k 2048 at 128 heads need more workspace than the
+    scratch array holds: SAS_ERR_SCRATCH, and nothing is launched (the tensor
+    block is never read)."""
+    from dsv4_planb_amd import _lib
+    from dsv4_planb_amd.metadata import plan_params
+
+    p = plan_params(total_tokens=8192, batch=1, num_heads_q=128, scenario=3, topk=2048,
+                    cmp_ratio=4, ori_win_left=127, core_num=256)
+    need = ctypes.c_size_t()
+    _lib.check(_lib.load().sas_workspace_size(ctypes.byref(p), ctypes.byref(need)))
+    assert need.value > _lib.SAS_SCRATCH_BYTES
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = _lib.load().sas_forward_noalloc(ctypes.byref(p), None, None, stream)
+    assert rc == -13, _lib.strerror(rc)
