@@ -100,6 +100,19 @@ class SasLaunch:
         and the outputs were zeroed.  Synchronises the device."""
         return int(self.ws[:4].view(torch.int32).item())
 
+    def run_attend_timed(self, start: torch.cuda.Event, stop: torch.cuda.Event):
+        """The attention stage alone, its dispatch recording its own start and end
+        into the two events (created with ``enable_timing=True``)."""
+        stream = torch.cuda.current_stream(self.device)
+        for e in (start, stop):  # torch creates the underlying event on first record
+            if not e.cuda_event:
+                e.record(stream)
+        rc = _lib.load().sas_attend_timed(
+            ctypes.byref(self.params), ctypes.byref(self.tensors), _ptr(self.plan), _ptr(self.ws),
+            self.ws.numel(), _stream_handle(self.device), ctypes.c_void_p(start.cuda_event),
+            ctypes.c_void_p(stop.cuda_event))
+        _lib.check(rc, "sas_attend_timed")
+
     def run(self, stage: str = "forward"):
         lib = _lib.load()
         fn = getattr(lib, f"sas_{stage}")

@@ -5,6 +5,7 @@
 // codes, workspace / plan sizing, and the stream-ordered launches of the
 // planner, resolver, attention and combine kernels.  Nothing here allocates
 // device memory or synchronises the host.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -274,8 +275,8 @@ int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   return launch_status();
 }
 
-int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
-               size_t ws_bytes, sas_stream_t stream) {
+int sas_attend_timed(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
+                     size_t ws_bytes, sas_stream_t stream, void* start_event, void* stop_event) {
   int rc = sas_validate(p);
   if (rc) return rc;
   if ((rc = check_tensors(p, t))) return rc;
@@ -285,10 +286,19 @@ int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pla
   if (!plan) plan = w.plan;
   if (p->total_tokens == 0) return SAS_OK;
   const SasFwdArgs a = fwd_args(p, target);
-  hipLaunchKernelGGL(pick_attend(p), dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream, a,
-                     static_cast<const uint16_t*>(t->q), w.addr, w.scale, w.ncmp, t->sinks, plan,
-                     static_cast<uint16_t*>(t->out), t->lse, w.o, w.ml);
+  // with events: the dispatch itself records its start and end into them
+  hipExtLaunchKernelGGL(pick_attend(p), dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream,
+                        (hipEvent_t)start_event, (hipEvent_t)stop_event, 0, a,
+                        static_cast<const uint16_t*>(t->q), static_cast<const uint64_t*>(w.addr),
+                        static_cast<const float*>(w.scale), static_cast<const int*>(w.ncmp),
+                        t->sinks, static_cast<const int*>(plan), static_cast<uint16_t*>(t->out),
+                        t->lse, w.o, w.ml);
   return launch_status();
+}
+
+int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
+               size_t ws_bytes, sas_stream_t stream) {
+  return sas_attend_timed(p, t, plan, ws, ws_bytes, stream, nullptr, nullptr);
 }
 
 int sas_combine(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,

@@ -156,6 +156,14 @@ int sas_combine(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
 #define SAS_SCRATCH_BYTES (160u << 20)
 int sas_forward_noalloc(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
                         sas_stream_t stream);
+/* sas_attend with the attention dispatch's own start and end recorded into two
+ * caller events (hipEvent_t created with timing; NULL: none): their elapsed time is
+ * the kernel's execution, without the gaps between back-to-back launches that
+ * events recorded on the stream around them include.  The device-side time of one
+ * launch, as profile_kernel.py:48-80 reads it on the reference's NPU. */
+int sas_attend_timed(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
+                     void* workspace, size_t workspace_bytes, sas_stream_t stream,
+                     void* start_event, void* stop_event);
 /* Debug: copy the resolved row-code lists of every token into rows (int32
  * [T, win_left + 1 (+ topk in scenarios 2, 3)]: the token's window pool rows, then
  * directly after them its compressed pool rows; -1 = a row read as zeros) and the
