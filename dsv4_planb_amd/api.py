@@ -113,6 +113,31 @@ class SasLaunch:
             ctypes.c_void_p(stop.cuda_event))
         _lib.check(rc, "sas_attend_timed")
 
+    def backward(self, dout: torch.Tensor, dlse: Optional[torch.Tensor] = None):
+        """Gradients for the queries and sinks of the last forward run through this
+        launch (its out / lse hold that call's results): ``(dq [T, H, d_qk] fp32,
+        dsinks [H] fp32)`` for ``dout = dL/dout`` ``[T, H, d_v]`` (and optionally
+        ``dlse = dL/dlse`` ``[T, H]``).  No gradient flows to the KV pools."""
+        lib = _lib.load()
+        p = self.params
+        T, H = p.total_tokens, p.num_heads_q
+        dev = self.device
+        q_dt = torch.bfloat16 if p.q_dtype == _lib.DT_BF16 else torch.float16
+        g = dout.to(device=dev, dtype=q_dt).reshape(T, H, p.head_dim_v).contiguous()
+        gl = None if dlse is None else dlse.to(device=dev, dtype=torch.float32).reshape(T, H).contiguous()
+        dq = torch.empty((T, H, p.head_dim_qk), dtype=torch.float32, device=dev)
+        dsinks = torch.empty(H, dtype=torch.float32, device=dev)
+        need = ctypes.c_size_t()
+        _lib.check(lib.sas_backward_workspace_size(ctypes.byref(p), ctypes.byref(need)),
+                   "sas_backward_workspace_size")
+        ws = torch.empty(int(need.value), dtype=torch.uint8, device=dev)
+        rc = lib.sas_backward(ctypes.byref(p), ctypes.byref(self.tensors), _ptr(self.plan),
+                              _ptr(g), _ptr(gl), _ptr(dq), _ptr(dsinks), _ptr(ws), ws.numel(),
+                              _stream_handle(dev))
+        _lib.check(rc, "sas_backward")
+        self._bwd_keep = (g, gl, ws)  # alive until the stream has used them
+        return dq, dsinks
+
     def run(self, stage: str = "forward"):
         lib = _lib.load()
         fn = getattr(lib, f"sas_{stage}")
@@ -328,6 +353,29 @@ class _SasKernelFunc:
         return out, lse
 
 
+class _SharedKVAttention(torch.autograd.Function):
+    """Autograd of the operator for the queries and the sinks: the forward is one
+    launch; the backward runs ``sas_backward`` on the same launch (same plan and row
+    lists) with the saved out / lse.  The KV pools get no gradient."""
+
+    @staticmethod
+    def forward(ctx, q_flat, sinks, spec):
+        launch, out, lse = build_launch(q_flat=q_flat.detach(), sinks=sinks.detach(), **spec)
+        launch.run()
+        ctx.launch = launch
+        ctx.q_dtype, ctx.sinks_dtype = q_flat.dtype, sinks.dtype
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        T, H = ctx.launch.params.total_tokens, ctx.launch.params.num_heads_q
+        if dout is None:
+            dout = torch.zeros((T, H, 512), dtype=ctx.q_dtype, device=ctx.launch.device)
+        dq, dsinks = ctx.launch.backward(dout, dlse)
+        return (dq.to(ctx.q_dtype) if ctx.needs_input_grad[0] else None,
+                dsinks.to(ctx.sinks_dtype) if ctx.needs_input_grad[1] else None, None)
+
+
 def sparse_attn_sharedkv(
     q: torch.Tensor,
     *,
@@ -356,7 +404,9 @@ def sparse_attn_sharedkv(
     cmp_kv_scale: Optional[torch.Tensor] = None,
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
     """Forward pass; returns ``attention_out`` in the layout of ``q`` (and the
-    fp32 LSE with the sink folded in when ``return_softmax_lse``).
+    fp32 LSE with the sink folded in when ``return_softmax_lse``).  When ``q`` or
+    ``sinks`` requires grad, the call is differentiable for them (the backward is
+    an extension: the reference has none).
 
     Scenario by optional inputs (api.py:156-160, 196-202): no ``cmp_kv`` -> SWA
     (1); ``cmp_kv`` without ``cmp_sparse_indices`` -> CFA (2); both -> SCFA (3).
@@ -410,14 +460,26 @@ def sparse_attn_sharedkv(
             raise ValueError(f"only N2=1 supported (got N2={N2})")
     cmp_ratio_eff = cmp_ratio if cmp_ratio is not None else 4
 
-    launch, out, lse = build_launch(
-        q_flat=q_flat, ori_kv=ori_kv, ori_block_table=ori_block_table,
+    spec = dict(
+        ori_kv=ori_kv, ori_block_table=ori_block_table,
         cmp_kv=cmp_kv, cmp_block_table=cmp_block_table, cmp_indices=idx,
-        q_prefix=q_prefix, act_q_lens=act_q, seqused_kv=seqused_kv, sinks=sinks,
+        q_prefix=q_prefix, act_q_lens=act_q, seqused_kv=seqused_kv,
         metadata=metadata, scenario=scenario, topk=K, cmp_ratio=cmp_ratio_eff,
         ori_win_left=ori_win_left, softmax_scale=softmax_scale, core_num=core_num,
         ori_kv_scale=ori_kv_scale, cmp_kv_scale=cmp_kv_scale)
-    launch.run()
+    grad = torch.is_grad_enabled() and (q.requires_grad or sinks.requires_grad)
+    if grad:
+        kv_grad = [n for n, x in (("ori_kv", ori_kv), ("cmp_kv", cmp_kv)) if x is not None and x.requires_grad]
+        if kv_grad:
+            raise NotImplementedError(
+                f"gradients for {', '.join(kv_grad)} are not implemented (the backward covers "
+                "the queries and the sinks); pass the KV cache detached")
+        if ori_kv.dtype == torch.float8_e4m3fn:
+            raise NotImplementedError("the backward supports 16-bit KV pools only")
+        out, lse = _SharedKVAttention.apply(q_flat, sinks, spec)
+    else:
+        launch, out, lse = build_launch(q_flat=q_flat, sinks=sinks, **spec)
+        launch.run()
 
     if layout_q == "BSND":
         out = out.reshape(B, S, out.shape[1], out.shape[2])

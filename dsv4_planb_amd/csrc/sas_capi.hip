@@ -16,6 +16,7 @@
 #include "sas_common.h"
 #include "sas_kernels.hip"
 #include "sas_attend.hip"
+#include "sas_backward.hip"
 
 namespace {
 
@@ -344,6 +345,77 @@ int sas_forward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   if ((rc = sas_resolve(p, t, plan, ws, ws_bytes, stream))) return rc;
   if ((rc = sas_attend(p, t, plan, ws, ws_bytes, stream))) return rc;
   return sas_combine(p, t, plan, ws, ws_bytes, stream);
+}
+
+int sas_backward_workspace_size(const sas_params_t* p, size_t* bytes) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if (!bytes) return SAS_ERR_NULL;
+  size_t fwd = 0;
+  if ((rc = sas_workspace_size(p, &fwd))) return rc;
+  const size_t th = (size_t)(p->total_tokens > 0 ? p->total_tokens : 1) * p->num_heads_q;
+  *bytes = fwd + 2 * sas_align256(th * 4);  // D and the sink term per (token, head)
+  return SAS_OK;
+}
+
+int sas_backward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
+                 const void* dout, const float* dlse, float* dq, float* dsinks, void* ws,
+                 size_t ws_bytes, sas_stream_t stream) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if ((rc = check_tensors(p, t))) return rc;
+  if (!dout || !dq || !dsinks || !t->lse) return SAS_ERR_NULL;
+  if (p->kv_dtype == SAS_DT_FP8E4M3) return SAS_ERR_NOT_IMPLEMENTED;
+  if (!aligned16(dout) || !aligned16(dq)) return SAS_ERR_SHAPE;
+  size_t need = 0;
+  if ((rc = sas_backward_workspace_size(p, &need))) return rc;
+  if (!ws || ws_bytes < need) return SAS_ERR_WORKSPACE;
+  const int target = target_units(p);
+  Ws w;
+  if ((rc = carve(p, ws, ws_bytes, target, &w))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const int T = p->total_tokens, H = p->num_heads_q;
+  const SasWsLayout W = sas_ws_layout(T, list_k(p), H, p->head_dim_v, target, p->scenario,
+                                      p->ori_win_left, false);
+  float* dterm = reinterpret_cast<float*>(static_cast<char*>(ws) + W.total);
+  float* sterm = reinterpret_cast<float*>(static_cast<char*>(ws) + W.total +
+                                          sas_align256((size_t)T * H * 4));
+  if (T == 0) {  // no tokens: dsinks = 0 (a kernel, not a memset, so the call can be captured)
+    hipLaunchKernelGGL(sas::bwd_dsink_kernel, dim3((H + 3) / 4), dim3(256), 0, s, 0, H,
+                       static_cast<const float*>(sterm), dsinks);
+    return launch_status();
+  }
+  if (!plan) {
+    hipLaunchKernelGGL(sas::plan_kernel, dim3(1), dim3(sas::PLAN_NT), 0, s, plan_args(p, target),
+                       t->q_prefix, t->act_q_lens, t->seqused_kv, w.plan);
+    if ((rc = launch_status())) return rc;
+    plan = w.plan;
+  }
+  if ((rc = sas_resolve(p, t, plan, ws, ws_bytes, stream))) return rc;
+  const SasFwdArgs a = fwd_args(p, target);
+  const bool f16 = p->q_dtype == SAS_DT_FP16;
+  if (f16)
+    hipLaunchKernelGGL(sas::bwd_prep_kernel<1>, dim3(T), dim3(256), 0, s, a, p->head_dim_qk, plan,
+                       static_cast<const uint16_t*>(dout), static_cast<const uint16_t*>(t->out),
+                       t->lse, dlse, t->sinks, dterm, sterm, dq);
+  else
+    hipLaunchKernelGGL(sas::bwd_prep_kernel<0>, dim3(T), dim3(256), 0, s, a, p->head_dim_qk, plan,
+                       static_cast<const uint16_t*>(dout), static_cast<const uint16_t*>(t->out),
+                       t->lse, dlse, t->sinks, dterm, sterm, dq);
+  if ((rc = launch_status())) return rc;
+  const dim3 grid(a.unit_cap * ((H + sas::BW_HEADS - 1) / sas::BW_HEADS));
+  typedef void (*bwd_fn_t)(SasFwdArgs, const uint16_t*, const uint16_t*, const uint64_t*,
+                           const int*, const float*, const float*, const int*, float*);
+  bwd_fn_t fn = p->head_dim_qk == 576 ? (f16 ? &sas::bwd_dq_kernel<576, 1> : &sas::bwd_dq_kernel<576, 0>)
+                                      : (f16 ? &sas::bwd_dq_kernel<512, 1> : &sas::bwd_dq_kernel<512, 0>);
+  hipLaunchKernelGGL(fn, grid, dim3(256), 0, s, a, static_cast<const uint16_t*>(t->q),
+                     static_cast<const uint16_t*>(dout), static_cast<const uint64_t*>(w.addr),
+                     static_cast<const int*>(w.ncmp), static_cast<const float*>(t->lse),
+                     static_cast<const float*>(dterm), plan, dq);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(sas::bwd_dsink_kernel, dim3((H + 3) / 4), dim3(256), 0, s, T, H,
+                     static_cast<const float*>(sterm), dsinks);
+  return launch_status();
 }
 
 int sas_debug_rows(const sas_params_t* p, const void* ws, int32_t* rows, int32_t* counts,

@@ -59,6 +59,9 @@ def load():
     lib.sasg_resolve.argtypes = [ctypes.POINTER(SasgParams), P, P, P, P, P, P, ctypes.c_int32,
                                  P, P, P]
     lib.sasg_resolve.restype = ctypes.c_int
+    lib.sasg_attention_bwd_exact.argtypes = [ctypes.POINTER(SasgParams), P, P, P, P, P, P, P, P,
+                                             P, P, P, P, P, P, ctypes.c_int32, P, P, P, P]
+    lib.sasg_attention_bwd_exact.restype = ctypes.c_int
     lib.sasg_round.argtypes = [ctypes.c_int, P, P, ctypes.c_int64]
     lib.sasg_round.restype = ctypes.c_int
     _lib = lib
@@ -216,3 +219,68 @@ def resolve(
     if rc != 0:
         raise ValueError(f"oracle resolve failed (code {rc})")
     return rows, n_ori, n_cmp
+
+
+def backward_exact(
+    *,
+    q: np.ndarray,
+    ori_kv: np.ndarray,
+    ori_block_table: np.ndarray,
+    q_prefix: Sequence[int],
+    act_q: Sequence[int],
+    seqused_kv: Sequence[int],
+    sinks: np.ndarray,
+    softmax_scale: float,
+    scenario: int,
+    dout: np.ndarray,  # [T, H, d_v] float32 values
+    cmp_kv: Optional[np.ndarray] = None,
+    cmp_block_table: Optional[np.ndarray] = None,
+    cmp_sparse_indices: Optional[np.ndarray] = None,
+    cmp_ratio: int = 4,
+    win_left: int = 127,
+    d_v: Optional[int] = None,
+    q_dtype: str = "bf16",
+    kv_dtype: str = "bf16",
+    ori_scale: Optional[np.ndarray] = None,
+    cmp_scale: Optional[np.ndarray] = None,
+    tokens: Optional[Sequence[int]] = None,
+    nthreads: int = 0,
+    kv_grad: bool = False,
+):
+    """The float64 backward of the exact forward over the same resolved rows:
+    ``(dq [T, H, D], dsinks [H], dori, dcmp)`` as float32 (the pool gradients in
+    the pools' [NB, BS, D] shape when ``kv_grad``, else None)."""
+    lib = load()
+    T, H, D = q.shape
+    d_v = D if d_v is None else d_v
+    B = len(act_q)
+    K = 0 if cmp_sparse_indices is None else cmp_sparse_indices.reshape(T, -1).shape[1]
+    qdt = np.float32 if q_dtype == "fp32" else np.uint16
+    kdt = {"fp32": np.float32, "bf16": np.uint16, "fp16": np.uint16, "fp8e4m3": np.uint8}[kv_dtype]
+    q_a = _c(q, qdt)
+    ori_a = _c(ori_kv, kdt)
+    cmp_a = _c(cmp_kv, kdt)
+    obt = _c(ori_block_table, np.int32)
+    cbt = _c(cmp_block_table, np.int32)
+    idx = _c(cmp_sparse_indices.reshape(T, -1) if cmp_sparse_indices is not None else None, np.int32)
+    tok = _c(np.asarray(tokens), np.int32) if tokens is not None else None
+    dq = np.zeros((T, H, D), np.float32)
+    ds = np.zeros(H, np.float32)
+    dori = np.zeros(ori_a.shape[:2] + (D,), np.float32) if kv_grad else None
+    dcmp = np.zeros(cmp_a.shape[:2] + (D,), np.float32) if (kv_grad and cmp_a is not None) else None
+    p = _params(T=T, H=H, D=D, Dv=d_v, B=B, scenario=scenario, win_left=win_left,
+                cmp_ratio=cmp_ratio, K=K, q_dtype=q_dtype, kv_dtype=kv_dtype,
+                ori_shape=ori_a.shape, ori_table_len=obt.shape[1],
+                cmp_shape=None if cmp_a is None else cmp_a.shape,
+                cmp_table_len=1 if cbt is None else cbt.shape[1],
+                softmax_scale=softmax_scale, nthreads=nthreads)
+    rc = lib.sasg_attention_bwd_exact(
+        ctypes.byref(p), _ptr(q_a), _ptr(ori_a), _ptr(_c(ori_scale, np.float32)), _ptr(obt),
+        _ptr(cmp_a), _ptr(_c(cmp_scale, np.float32)), _ptr(cbt), _ptr(idx),
+        _ptr(_c(np.asarray(q_prefix), np.int32)), _ptr(_c(np.asarray(act_q), np.int32)),
+        _ptr(_c(np.asarray(seqused_kv), np.int32)), _ptr(_c(sinks, np.float32)),
+        _ptr(_c(dout, np.float32)), _ptr(tok), 0 if tok is None else len(tok), _ptr(dq), _ptr(ds),
+        _ptr(dori), _ptr(dcmp))
+    if rc != 0:
+        raise ValueError(f"oracle rejected the inputs (code {rc})")
+    return dq, ds, dori, dcmp

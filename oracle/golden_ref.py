@@ -340,3 +340,116 @@ def sinks_softmax_reference_f64(
         out = (y / denom) @ k
         lse = (x_max + np.log(denom))[:, 0]
     return out, lse
+
+
+# --------------------------------------------------------------------------
+# Backward (no counterpart in the reference, which keeps the LSE for one:
+# api.py:32-35, 176-184).  The gradient of the one-shot sink softmax over the
+# same resolved rows, float64: with P_j = e^(s_j - lse), s_j = scale <q, K_j>,
+# V_j = K_j[:d_v], out = sum_j P_j V_j and P_sink = e^(sink - lse):
+#   D = <dO, out>,  dP_j = <dO, V_j>,  dS_j = P_j (dP_j - D)
+#   dq = scale sum_j dS_j K_j,  dsink = -P_sink D,
+#   dK_j += scale dS_j q,  dV_j += P_j dO  (V is the leading d_v columns of the
+#   same row, so both land in that row's gradient).
+# --------------------------------------------------------------------------
+def golden_backward_f64(
+    *,
+    q: np.ndarray,  # [T, H, Dqk] values (float)
+    ori_kv: np.ndarray,  # [NB1, BS1, Dqk] values
+    ori_block_table: np.ndarray,
+    q_prefix: Sequence[int],
+    act_q: Sequence[int],
+    seqused_kv: Sequence[int],
+    sinks: np.ndarray,
+    softmax_scale: float,
+    scenario: int,
+    dout: np.ndarray,  # [T, H, d_v]
+    cmp_kv: Optional[np.ndarray] = None,
+    cmp_block_table: Optional[np.ndarray] = None,
+    cmp_sparse_indices: Optional[np.ndarray] = None,
+    cmp_ratio: int = 4,
+    win_left: int = 127,
+    d_v: Optional[int] = None,
+):
+    """Returns ``(dq [T, H, Dqk], dsinks [H], dori [NB1, BS1, Dqk], dcmp or None)``
+    in float64.  Rows read as zeros (unused pages) receive no gradient."""
+    T, H, Dqk = q.shape
+    d_v = Dqk if d_v is None else d_v
+    dq = np.zeros((T, H, Dqk), np.float64)
+    dsinks = np.zeros(H, np.float64)
+    ori_flat = ori_kv.reshape(-1, Dqk).astype(np.float64)
+    cmp_flat = None if cmp_kv is None else cmp_kv.reshape(-1, Dqk).astype(np.float64)
+    dori = np.zeros_like(ori_flat)
+    dcmp = None if cmp_flat is None else np.zeros_like(cmp_flat)
+    BS1 = ori_kv.shape[1]
+    BS2 = 1 if cmp_kv is None else cmp_kv.shape[1]
+    sk = np.asarray(sinks, np.float64)
+    for b in range(len(act_q)):
+        aq, akv = int(act_q[b]), int(seqused_kv[b])
+        for s in range(aq):
+            t = int(q_prefix[b]) + s
+            ori_rows, cmp_rows = token_rows(
+                b=b, s_local=s, act_q=aq, act_kv=akv, scenario=scenario,
+                ori_block_table=ori_block_table, ori_block_size=BS1,
+                cmp_block_table=cmp_block_table, cmp_block_size=BS2,
+                idx_row=None if cmp_sparse_indices is None else cmp_sparse_indices[t],
+                cmp_ratio=cmp_ratio, win_left=win_left)
+            src = [(ori_flat, dori, r) for r in ori_rows] + [(cmp_flat, dcmp, r) for r in cmp_rows]
+            K = np.array([pool[r] if r >= 0 else np.zeros(Dqk) for pool, _, r in src]).reshape(-1, Dqk)
+            qt = q[t].astype(np.float64)  # [H, Dqk]
+            s_ = softmax_scale * (qt @ K.T)  # [H, n]
+            m = np.maximum(sk, s_.max(axis=1) if s_.shape[1] else -np.inf)
+            m = np.where(np.isfinite(m), m, 0.0)  # a head with nothing to attend: all zero
+            e = np.exp(s_ - m[:, None])
+            es = np.where(np.isneginf(sk), 0.0, np.exp(np.where(np.isneginf(sk), 0.0, sk) - m))
+            l = es + e.sum(axis=1)
+            safe = np.where(l > 0, l, 1.0)
+            P = e / safe[:, None]
+            Ps = es / safe
+            V = K[:, :d_v]
+            out = P @ V  # [H, d_v]
+            dO = dout[t].astype(np.float64)
+            Dh = (dO * out).sum(axis=1)
+            dP = dO @ V.T
+            dS = P * (dP - Dh[:, None])
+            dq[t] = softmax_scale * (dS @ K)
+            dsinks -= Ps * Dh
+            gK = softmax_scale * (dS.T @ qt)  # [n, Dqk]
+            gK[:, :d_v] += P.T @ dO
+            for j, (_, grad, r) in enumerate(src):
+                if r >= 0:
+                    grad[r] += gK[j]
+    dori = dori.reshape(ori_kv.shape)
+    if dcmp is not None:
+        dcmp = dcmp.reshape(cmp_kv.shape)
+    return dq, dsinks, dori, dcmp
+
+
+def golden_forward_f64(*, q, ori_kv, ori_block_table, q_prefix, act_q, seqused_kv, sinks,
+                       softmax_scale, scenario, cmp_kv=None, cmp_block_table=None,
+                       cmp_sparse_indices=None, cmp_ratio=4, win_left=127, d_v=None):
+    """The one-shot sink softmax over the resolved rows in float64 (no rounding):
+    ``out [T, H, d_v]``, the function golden_backward_f64 differentiates."""
+    T, H, Dqk = q.shape
+    d_v = Dqk if d_v is None else d_v
+    out = np.zeros((T, H, d_v), np.float64)
+    ori_flat = ori_kv.reshape(-1, Dqk)
+    cmp_flat = None if cmp_kv is None else cmp_kv.reshape(-1, Dqk)
+    BS1 = ori_kv.shape[1]
+    BS2 = 1 if cmp_kv is None else cmp_kv.shape[1]
+    for b in range(len(act_q)):
+        aq, akv = int(act_q[b]), int(seqused_kv[b])
+        for s in range(aq):
+            t = int(q_prefix[b]) + s
+            ori_rows, cmp_rows = token_rows(
+                b=b, s_local=s, act_q=aq, act_kv=akv, scenario=scenario,
+                ori_block_table=ori_block_table, ori_block_size=BS1,
+                cmp_block_table=cmp_block_table, cmp_block_size=BS2,
+                idx_row=None if cmp_sparse_indices is None else cmp_sparse_indices[t],
+                cmp_ratio=cmp_ratio, win_left=win_left)
+            rows = [(ori_flat, r) for r in ori_rows] + [(cmp_flat, r) for r in cmp_rows]
+            K = np.array([pool[r] if r >= 0 else np.zeros(Dqk) for pool, r in rows],
+                         np.float64).reshape(-1, Dqk)
+            o, _ = sinks_softmax_reference_f64(q[t], K, sinks, softmax_scale)
+            out[t] = o[:, :d_v]
+    return out

@@ -418,6 +418,130 @@ int sasg_attention_exact(const sasg_params* p, const void* q, const void* ori_kv
   return err;
 }
 
+/* Backward of the one-shot sink softmax over the same resolved rows, in double
+ * (the reference has no backward; this is the gradient of sasg_attention_exact):
+ * with P_j = e^(s_j - lse), out = sum_j P_j V_j, P_sink = e^(sink - lse),
+ *   D = <dO, out>, dS_j = P_j (<dO, V_j> - D),
+ *   dq = scale sum_j dS_j K_j, dsink = -sum_t P_sink D,
+ *   dK_j += scale dS_j q, dV_j += P_j dO (both into the row's gradient).
+ * dout [T, H, Dv] float; dq [T, H, D] float; dsinks [H] float; dori / dcmp
+ * (float, the pools' shapes, zeroed by the caller) may be NULL.  Tokens listed
+ * in `tokens` (all when NULL) are differentiated; the others' dq stays as given. */
+int sasg_attention_bwd_exact(const sasg_params* p, const void* q, const void* ori_kv,
+                             const float* ori_scale, const int32_t* ori_bt, const void* cmp_kv,
+                             const float* cmp_scale, const int32_t* cmp_bt, const int32_t* idx,
+                             const int32_t* q_prefix, const int32_t* act_q,
+                             const int32_t* seqused_kv, const float* sinks, const float* dout,
+                             const int32_t* tokens, int32_t n_tokens, float* dq, float* dsinks,
+                             float* dori, float* dcmp) {
+  const int H = p->H, D = p->D, Dv = p->Dv;
+  int32_t* tb = (int32_t*)malloc(sizeof(int32_t) * (p->T > 0 ? p->T : 1));
+  int32_t* ts = (int32_t*)malloc(sizeof(int32_t) * (p->T > 0 ? p->T : 1));
+  double* sterm = (double*)calloc((size_t)(p->T > 0 ? p->T : 1) * H, sizeof(double));
+  build_token_map(p, q_prefix, act_q, tb, ts);
+  int nwork = tokens ? n_tokens : p->T;
+  int need = max_rows_per_token(p, seqused_kv);
+  int err = 0;
+#ifdef _OPENMP
+  if (p->nthreads > 0) omp_set_num_threads(p->nthreads);
+#endif
+#pragma omp parallel
+  {
+    int64_t* rows = (int64_t*)malloc(sizeof(int64_t) * need);
+    int* is_cmp = (int*)malloc(sizeof(int) * need);
+    double* kv = (double*)malloc(sizeof(double) * (size_t)need * D);
+    double* sc = (double*)malloc(sizeof(double) * (size_t)need);
+    double* qh = (double*)malloc(sizeof(double) * (size_t)D);
+    double* oh = (double*)malloc(sizeof(double) * (size_t)Dv);
+    double* gq = (double*)malloc(sizeof(double) * (size_t)D);
+#pragma omp for schedule(dynamic, 1)
+    for (int w = 0; w < nwork; ++w) {
+      int t = tokens ? tokens[w] : w;
+      if (t < 0 || t >= p->T) continue;
+      float* dqt = dq + (int64_t)t * H * D;
+      memset(dqt, 0, sizeof(float) * (size_t)H * D);
+      if (tb[t] < 0) continue;
+      int b = tb[t], no, nc;
+      if (resolve_token(p, ori_bt, cmp_bt, idx, b, t, ts[t], act_q[b], seqused_kv[b], rows, &no,
+                        &nc)) {
+#pragma omp atomic write
+        err = -1;
+        continue;
+      }
+      int n = no + nc;
+      for (int j = 0; j < n; ++j) {
+        is_cmp[j] = j >= no;
+        int64_t row = rows[j];
+        double* kr = kv + (int64_t)j * D;
+        if (row < 0) { for (int d = 0; d < D; ++d) kr[d] = 0.0; continue; }
+        const void* pool = is_cmp[j] ? cmp_kv : ori_kv;
+        int bs = is_cmp[j] ? p->cmp_block_size : p->ori_block_size;
+        int64_t base = (row / bs) * (is_cmp[j] ? p->cmp_block_stride : p->ori_block_stride) +
+                       (row % bs) * (is_cmp[j] ? p->cmp_row_stride : p->ori_row_stride);
+        float scl = 1.0f;
+        if (p->kv_dtype == SASG_FP8E4M3) scl = (is_cmp[j] ? cmp_scale : ori_scale)[row];
+        for (int d = 0; d < D; ++d) {
+          float v = load_elem(pool, p->kv_dtype, base + d);
+          kr[d] = p->kv_dtype == SASG_FP8E4M3 ? (double)(v * scl) : (double)v;
+        }
+      }
+      for (int h = 0; h < H; ++h) {
+        for (int d = 0; d < D; ++d) qh[d] = load_elem(q, p->q_dtype, ((int64_t)t * H + h) * D + d);
+        const float* doh = dout + ((int64_t)t * H + h) * Dv;
+        double m = sinks[h];
+        for (int j = 0; j < n; ++j) {
+          const double* kr = kv + (int64_t)j * D;
+          double dot = 0.0;
+          for (int d = 0; d < D; ++d) dot += qh[d] * kr[d];
+          sc[j] = dot * (double)p->softmax_scale;
+          if (sc[j] > m) m = sc[j];
+        }
+        if (isinf(m) && m < 0) m = 0.0; /* a head with nothing to attend: all zero */
+        double es = isinf(sinks[h]) && sinks[h] < 0 ? 0.0 : exp((double)sinks[h] - m);
+        double l = es;
+        for (int j = 0; j < n; ++j) { sc[j] = exp(sc[j] - m); l += sc[j]; }
+        if (l <= 0.0) l = 1.0;
+        for (int d = 0; d < Dv; ++d) oh[d] = 0.0;
+        for (int j = 0; j < n; ++j) {
+          sc[j] /= l; /* P_j */
+          const double* kr = kv + (int64_t)j * D;
+          for (int d = 0; d < Dv; ++d) oh[d] += sc[j] * kr[d];
+        }
+        double Dh = 0.0;
+        for (int d = 0; d < Dv; ++d) Dh += (double)doh[d] * oh[d];
+        sterm[(int64_t)t * H + h] = -(es / l) * Dh;
+        for (int d = 0; d < D; ++d) gq[d] = 0.0;
+        for (int j = 0; j < n; ++j) {
+          const double* kr = kv + (int64_t)j * D;
+          double dp = 0.0;
+          for (int d = 0; d < Dv; ++d) dp += (double)doh[d] * kr[d];
+          double ds = sc[j] * (dp - Dh);
+          for (int d = 0; d < D; ++d) gq[d] += ds * kr[d];
+          float* grad = is_cmp[j] ? dcmp : dori;
+          if (grad && rows[j] >= 0) {
+            int bs = is_cmp[j] ? p->cmp_block_size : p->ori_block_size;
+            int64_t gb = (rows[j] / bs) * (int64_t)bs * D + (rows[j] % bs) * (int64_t)D;
+            for (int d = 0; d < D; ++d) {
+              double g = (double)p->softmax_scale * ds * qh[d] + (d < Dv ? sc[j] * doh[d] : 0.0);
+#pragma omp atomic
+              grad[gb + d] += (float)g;
+            }
+          }
+        }
+        for (int d = 0; d < D; ++d) dqt[(int64_t)h * D + d] = (float)((double)p->softmax_scale * gq[d]);
+      }
+    }
+    free(rows); free(is_cmp); free(kv); free(sc); free(qh); free(oh); free(gq);
+  }
+  for (int h = 0; h < H; ++h) {
+    double acc = 0.0;
+    for (int t = 0; t < p->T; ++t) acc += sterm[(int64_t)t * H + h];
+    dsinks[h] = (float)acc;
+  }
+  free(tb); free(ts); free(sterm);
+  return err;
+}
+
 /* Test hook: the oracle's own rounding of n floats to the dtype dt (SASG_BF16 or
  * SASG_F16; other codes copy), so its rounding can be checked against a library. */
 int sasg_round(int dt, const float* x, float* y, int64_t n) {
