@@ -109,7 +109,7 @@ def load():
         lib.sas_forward_noalloc.argtypes = [PP, PT, P, P]
         lib.sas_attend_timed.argtypes = [PP, PT, P, P, S, P, P, P]
         lib.sas_backward_workspace_size.argtypes = [PP, ctypes.POINTER(S)]
-        lib.sas_backward.argtypes = [PP, PT, P, P, P, P, P, P, S, P]
+        lib.sas_backward.argtypes = [PP, PT, P, P, P, P, P, P, P, P, S, P]
         lib.sas_graph_capture.argtypes = [PP, PT, P, P, S, P, ctypes.POINTER(P)]
         lib.sas_graph_launch.argtypes = [P, P]
         lib.sas_graph_destroy.argtypes = [P]

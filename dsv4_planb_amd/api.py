@@ -93,6 +93,8 @@ class SasLaunch:
         self.plan = plan
         self.ws = ws
         self.device = device
+        self.ori_kv = None  # the pools (their shapes and strides lay out the KV gradient)
+        self.cmp_kv = None
 
     def device_status(self) -> int:
         """The workspace status word of the last forward call: 0, or -8
@@ -113,11 +115,13 @@ class SasLaunch:
             ctypes.c_void_p(stop.cuda_event))
         _lib.check(rc, "sas_attend_timed")
 
-    def backward(self, dout: torch.Tensor, dlse: Optional[torch.Tensor] = None):
-        """Gradients for the queries and sinks of the last forward run through this
-        launch (its out / lse hold that call's results): ``(dq [T, H, d_qk] fp32,
-        dsinks [H] fp32)`` for ``dout = dL/dout`` ``[T, H, d_v]`` (and optionally
-        ``dlse = dL/dlse`` ``[T, H]``).  No gradient flows to the KV pools."""
+    def backward(self, dout: torch.Tensor, dlse: Optional[torch.Tensor] = None,
+                 kv_grad: bool = False):
+        """Gradients of the last forward run through this launch (its out / lse hold
+        that call's results) for ``dout = dL/dout`` ``[T, H, d_v]`` (and optionally
+        ``dlse = dL/dlse`` ``[T, H]``): ``(dq [T, H, d_qk] fp32, dsinks [H] fp32)``,
+        and with ``kv_grad`` also ``(d_ori_kv, d_cmp_kv)``: fp32 tensors with the
+        pools' shapes and strides (``d_cmp_kv`` None in scenario 1)."""
         lib = _lib.load()
         p = self.params
         T, H = p.total_tokens, p.num_heads_q
@@ -131,11 +135,22 @@ class SasLaunch:
         _lib.check(lib.sas_backward_workspace_size(ctypes.byref(p), ctypes.byref(need)),
                    "sas_backward_workspace_size")
         ws = torch.empty(int(need.value), dtype=torch.uint8, device=dev)
+        d_ori = d_cmp = None
+        if kv_grad:
+            # laid out like the pools (same strides, so padded pools work), zeroed:
+            # the kernel adds into them
+            d_ori = torch.empty_strided(self.ori_kv.shape, self.ori_kv.stride(),
+                                        dtype=torch.float32, device=dev).zero_()
+            if p.scenario >= 2 and self.cmp_kv is not None:
+                d_cmp = torch.empty_strided(self.cmp_kv.shape, self.cmp_kv.stride(),
+                                            dtype=torch.float32, device=dev).zero_()
         rc = lib.sas_backward(ctypes.byref(p), ctypes.byref(self.tensors), _ptr(self.plan),
-                              _ptr(g), _ptr(gl), _ptr(dq), _ptr(dsinks), _ptr(ws), ws.numel(),
-                              _stream_handle(dev))
+                              _ptr(g), _ptr(gl), _ptr(dq), _ptr(dsinks), _ptr(d_ori), _ptr(d_cmp),
+                              _ptr(ws), ws.numel(), _stream_handle(dev))
         _lib.check(rc, "sas_backward")
         self._bwd_keep = (g, gl, ws)  # alive until the stream has used them
+        if kv_grad:
+            return dq, dsinks, d_ori, d_cmp
         return dq, dsinks
 
     def run(self, stage: str = "forward"):
@@ -282,7 +297,9 @@ def build_launch(
     t.ori_kv_scale = osc.data_ptr() if osc is not None else None
     t.cmp_kv_scale = csc.data_ptr() if csc is not None else None
     t.out, t.lse = out.data_ptr(), lse.data_ptr()
-    return SasLaunch(p, t, keep, plan, ws, dev), out, lse
+    launch = SasLaunch(p, t, keep, plan, ws, dev)
+    launch.ori_kv, launch.cmp_kv = ori_kv, cmp_kv
+    return launch, out, lse
 
 
 def _get_kernel(
@@ -354,16 +371,19 @@ class _SasKernelFunc:
 
 
 class _SharedKVAttention(torch.autograd.Function):
-    """Autograd of the operator for the queries and the sinks: the forward is one
-    launch; the backward runs ``sas_backward`` on the same launch (same plan and row
-    lists) with the saved out / lse.  The KV pools get no gradient."""
+    """Autograd of the operator for the queries, the sinks and the two KV pools:
+    the forward is one launch; the backward runs ``sas_backward`` on the same launch
+    (same plan and row lists) with the saved out / lse."""
 
     @staticmethod
-    def forward(ctx, q_flat, sinks, spec):
-        launch, out, lse = build_launch(q_flat=q_flat.detach(), sinks=sinks.detach(), **spec)
+    def forward(ctx, q_flat, sinks, ori_kv, cmp_kv, spec):
+        launch, out, lse = build_launch(
+            q_flat=q_flat.detach(), sinks=sinks.detach(), ori_kv=ori_kv.detach(),
+            cmp_kv=None if cmp_kv is None else cmp_kv.detach(), **spec)
         launch.run()
         ctx.launch = launch
         ctx.q_dtype, ctx.sinks_dtype = q_flat.dtype, sinks.dtype
+        ctx.kv_dtype = ori_kv.dtype
         return out, lse
 
     @staticmethod
@@ -371,9 +391,15 @@ class _SharedKVAttention(torch.autograd.Function):
         T, H = ctx.launch.params.total_tokens, ctx.launch.params.num_heads_q
         if dout is None:
             dout = torch.zeros((T, H, 512), dtype=ctx.q_dtype, device=ctx.launch.device)
-        dq, dsinks = ctx.launch.backward(dout, dlse)
+        kv = ctx.needs_input_grad[2] or ctx.needs_input_grad[3]
+        res = ctx.launch.backward(dout, dlse, kv_grad=kv)
+        dq, dsinks = res[0], res[1]
+        d_ori = res[2] if kv and ctx.needs_input_grad[2] else None
+        d_cmp = res[3] if kv and ctx.needs_input_grad[3] and res[3] is not None else None
         return (dq.to(ctx.q_dtype) if ctx.needs_input_grad[0] else None,
-                dsinks.to(ctx.sinks_dtype) if ctx.needs_input_grad[1] else None, None)
+                dsinks.to(ctx.sinks_dtype) if ctx.needs_input_grad[1] else None,
+                None if d_ori is None else d_ori.to(ctx.kv_dtype),
+                None if d_cmp is None else d_cmp.to(ctx.kv_dtype), None)
 
 
 def sparse_attn_sharedkv(
@@ -461,24 +487,20 @@ def sparse_attn_sharedkv(
     cmp_ratio_eff = cmp_ratio if cmp_ratio is not None else 4
 
     spec = dict(
-        ori_kv=ori_kv, ori_block_table=ori_block_table,
-        cmp_kv=cmp_kv, cmp_block_table=cmp_block_table, cmp_indices=idx,
+        ori_block_table=ori_block_table, cmp_block_table=cmp_block_table, cmp_indices=idx,
         q_prefix=q_prefix, act_q_lens=act_q, seqused_kv=seqused_kv,
         metadata=metadata, scenario=scenario, topk=K, cmp_ratio=cmp_ratio_eff,
         ori_win_left=ori_win_left, softmax_scale=softmax_scale, core_num=core_num,
         ori_kv_scale=ori_kv_scale, cmp_kv_scale=cmp_kv_scale)
-    grad = torch.is_grad_enabled() and (q.requires_grad or sinks.requires_grad)
+    grad = torch.is_grad_enabled() and any(
+        x is not None and x.requires_grad for x in (q, sinks, ori_kv, cmp_kv))
     if grad:
-        kv_grad = [n for n, x in (("ori_kv", ori_kv), ("cmp_kv", cmp_kv)) if x is not None and x.requires_grad]
-        if kv_grad:
-            raise NotImplementedError(
-                f"gradients for {', '.join(kv_grad)} are not implemented (the backward covers "
-                "the queries and the sinks); pass the KV cache detached")
         if ori_kv.dtype == torch.float8_e4m3fn:
             raise NotImplementedError("the backward supports 16-bit KV pools only")
-        out, lse = _SharedKVAttention.apply(q_flat, sinks, spec)
+        out, lse = _SharedKVAttention.apply(q_flat, sinks, ori_kv, cmp_kv, spec)
     else:
-        launch, out, lse = build_launch(q_flat=q_flat, sinks=sinks, **spec)
+        launch, out, lse = build_launch(q_flat=q_flat, sinks=sinks, ori_kv=ori_kv, cmp_kv=cmp_kv,
+                                        **spec)
         launch.run()
 
     if layout_q == "BSND":

@@ -1,4 +1,5 @@
-// sas_backward.hip -- gfx950 kernels of the backward pass for the queries and sinks.
+// sas_backward.hip -- gfx950 kernels of the backward pass: queries, sinks and the
+// KV pools.
 //
 // The reference has no backward; it returns the LSE for one (api.py:32-35,
 // 176-184).  With the forward's out and lse, P_j = e^(s_j - lse) is known exactly
@@ -16,6 +17,8 @@
 //                     registers), P and dS in registers, then dq^T += K^T dS^T
 //                     (K^T from a transposed LDS copy of the tile, dS^T straight
 //                     from the accumulator layout).
+//   bwd_dkv_kernel    the KV pools' gradient (dK from dS and q, dV from P and
+//                     dO), fp32 atomics into pool-shaped buffers.
 //   bwd_dsink_kernel  dsink[h] summed over tokens in a fixed order (one wave per
 //                     head), so it is deterministic.
 //
@@ -220,6 +223,180 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(SasFwdArgs a, const uint
       atomicAdd(dqr + 16 * db + 3, v.w);
     } else {
       *reinterpret_cast<float4*>(dqr + 16 * db) = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The KV pools' gradient.  Row j of token t's list (pool row R_j) receives
+//   dK_j = scale sum_h dS_hj q_h  (all d_qk dimensions)  +  dV_j = sum_h P_hj dO_h
+// (the first d_v dimensions), summed over every token and list position that reads
+// R_j (window overlap, repeated top-k ids): fp32 atomics into a gradient buffer
+// laid out like the pool (same block and row strides, in elements).  Rows read as
+// zeros (-1 codes) and rows past a unit's end receive nothing.
+//
+// One workgroup per (work unit, 32 heads).  The group's Q and dO are staged
+// transposed in LDS once ([dimension][head], 80-B rows), so a 16-B read is 8 heads
+// of one dimension.  Per 32-row tile:
+//   phase A  wave w computes S^T and dP^T for keys 16 (w & 1) .. + 15 and heads
+//            16 (w >> 1) .. + 15 of the group (16x16x32 MFMAs, K rows from the
+//            LDS tile, Q^T / dO^T fragments in registers), then P = e^(S - lse) and
+//            dS = P (dP - D), written to LDS as dS^T and P^T ([key][head], rounded
+//            to the query dtype)
+//   phase B  G = scale dS^T Q + P^T dO (keys x dimensions, 32 heads contracted in
+//            one MFMA per 16 x 16 block): wave w takes key block w & 1 and half of
+//            the dimension blocks; each lane then holds 4 keys of one dimension and
+//            adds them to the pool rows (16 lanes: 16 consecutive dimensions).
+// ---------------------------------------------------------------------------
+constexpr int DK_HEADS = 32;  // heads per workgroup
+
+template <int DQK, int QT>
+__global__ __launch_bounds__(256, 1) void bwd_dkv_kernel(
+    SasFwdArgs a, const uint16_t* __restrict__ q, const uint16_t* __restrict__ dout,
+    const uint64_t* __restrict__ addr_list, const int* __restrict__ row_codes,
+    const int* __restrict__ ncmp, const float* __restrict__ lse, const float* __restrict__ dterm,
+    const int* __restrict__ plan, float* __restrict__ d_ori, float* __restrict__ d_cmp) {
+  constexpr int DV = 512;
+  constexpr int KS = DQK / 32;         // k-steps of S^T = K Q^T (18 / 16)
+  constexpr int VKS = DV / 32;         // k-steps of dP^T = V dO^T (16)
+  constexpr int NDB = DQK / 16;        // 16-dimension blocks of G (36 / 32)
+  constexpr int CH = DQK / 8;          // 16-B chunks per row
+  constexpr int KSTR = DQK * 2 + 16;   // row-major tile: row stride in bytes
+  constexpr int TS = 2 * DK_HEADS + 16;  // transposed rows: bytes per dimension / key
+  __shared__ __attribute__((aligned(16))) uint8_t kt[BW_TILE * KSTR];
+  __shared__ __attribute__((aligned(16))) uint8_t qtr[DQK * TS];
+  __shared__ __attribute__((aligned(16))) uint8_t otr[DV * TS];
+  __shared__ __attribute__((aligned(16))) uint8_t dst[BW_TILE * TS];
+  __shared__ __attribute__((aligned(16))) uint8_t ptr[BW_TILE * TS];
+
+  const int HG = (a.H + DK_HEADS - 1) / DK_HEADS;
+  const int u = blockIdx.x / HG, hg = blockIdx.x - u * HG;
+  if (!plan_matches(plan, a) || u >= plan[PH_UNITS]) return;
+  const int* ur = plan + SAS_PLAN_HDR + (size_t)SAS_TOK_W * a.T + (size_t)u * SAS_UNIT_W;
+  const int t = ur[0], split = ur[3];
+  if (split < 0) return;  // a q row no batch owns: it reads no rows
+  const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
+  const int nwin = min(tk[TK_NWIN], a.win_left + 1);
+  const int r0 = ur[1];
+  const int r1 = min(min(ur[2], nwin + ncmp[t]), a.list_stride);
+  const int ntiles = r1 > r0 ? (r1 - r0 + BW_TILE - 1) / BW_TILE : 0;
+  if (ntiles == 0) return;
+  const uint64_t* alist = addr_list + (size_t)t * a.list_stride;
+  const int* codes = row_codes + (size_t)t * a.list_stride;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int n16 = lane & 15, g = lane >> 4;
+  const int h0 = hg * DK_HEADS;
+
+  // the group's Q and dO, transposed ([dimension][head]; heads past H are zeros)
+  for (int i = tid; i < DK_HEADS * CH; i += 256) {
+    const int hh = i / CH, cc = i - hh * CH;
+    u32x4_t v = u32x4_t{0, 0, 0, 0};
+    if (h0 + hh < a.H) v = reinterpret_cast<const u32x4_t*>(q + ((size_t)t * a.H + h0 + hh) * DQK)[cc];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      *reinterpret_cast<uint16_t*>(qtr + (8 * cc + 2 * e) * TS + 2 * hh) = (uint16_t)(v[e] & 0xffffu);
+      *reinterpret_cast<uint16_t*>(qtr + (8 * cc + 2 * e + 1) * TS + 2 * hh) = (uint16_t)(v[e] >> 16);
+    }
+  }
+  for (int i = tid; i < DK_HEADS * (DV / 8); i += 256) {
+    const int hh = i / (DV / 8), cc = i - hh * (DV / 8);
+    u32x4_t v = u32x4_t{0, 0, 0, 0};
+    if (h0 + hh < a.H) v = reinterpret_cast<const u32x4_t*>(dout + ((size_t)t * a.H + h0 + hh) * DV)[cc];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      *reinterpret_cast<uint16_t*>(otr + (8 * cc + 2 * e) * TS + 2 * hh) = (uint16_t)(v[e] & 0xffffu);
+      *reinterpret_cast<uint16_t*>(otr + (8 * cc + 2 * e + 1) * TS + 2 * hh) = (uint16_t)(v[e] >> 16);
+    }
+  }
+
+  // phase A role: keys 16 kb .. + 15, heads hl = 16 hb + n16 of the group
+  const int kb = w & 1, hb = w >> 1;
+  const int hl = 16 * hb + n16, h = h0 + hl;
+  const bool hvalid = h < a.H;
+  const int hc = min(h, a.H - 1);
+  const size_t th = (size_t)t * a.H + hc;
+  u32x4_t qf[KS], of[VKS];
+  {
+    const u32x4_t* qr = reinterpret_cast<const u32x4_t*>(q + th * DQK);
+    const u32x4_t* orow = reinterpret_cast<const u32x4_t*>(dout + th * DV);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = qr[4 * ks + g];
+#pragma unroll
+    for (int ks = 0; ks < VKS; ++ks) of[ks] = orow[4 * ks + g];
+  }
+  const float lse2 = lse[th] * LOG2E, dh = dterm[th];
+  const float c = a.scale_log2;
+  const float scale = c * 0.6931471805599453f;
+  // phase B role: key block kb (as in phase A), dimension blocks [db0, db0 + NDB / 2)
+  const int db0 = hb * (NDB / 2);
+
+  for (int i = 0; i < ntiles; ++i) {
+    const int rb = r0 + i * BW_TILE;
+    __syncthreads();  // every wave is done with the previous tile (and the staging)
+    for (int ch = tid; ch < BW_TILE * CH; ch += 256) {
+      const int row = ch / CH, cc = ch - row * CH;
+      u32x4_t v = u32x4_t{0, 0, 0, 0};
+      if (rb + row < r1) v = reinterpret_cast<const u32x4_t*>(alist[rb + row])[cc];
+      *reinterpret_cast<u32x4_t*>(kt + row * KSTR + cc * 16) = v;
+    }
+    __syncthreads();
+    // phase A: S^T and dP^T of 16 keys x 16 heads; lane holds keys 16 kb + 4 g + r
+    {
+      const uint8_t* kr = kt + (16 * kb + n16) * KSTR + 16 * g;
+      bw_f32x4 s = bw_f32x4{0.f, 0.f, 0.f, 0.f}, dp = s;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const u32x4_t av = *reinterpret_cast<const u32x4_t*>(kr + 64 * ks);
+        s = bw_mfma<QT>(av, qf[ks], s);
+        if (ks < VKS) dp = bw_mfma<QT>(av, of[ks], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = 16 * kb + 4 * g + r;
+        const bool valid = hvalid && rb + key < r1;
+        const float p = valid ? exp2f(fmaf(s[r], c, -lse2)) : 0.f;
+        const float ds = p * (dp[r] - dh);
+        const uint32_t pk = pack2_q16<QT>(ds, p);
+        *reinterpret_cast<uint16_t*>(dst + key * TS + 2 * hl) = (uint16_t)(pk & 0xffffu);
+        *reinterpret_cast<uint16_t*>(ptr + key * TS + 2 * hl) = (uint16_t)(pk >> 16);
+      }
+    }
+    __syncthreads();
+    // phase B: G = scale dS^T Q + P^T dO for keys 16 kb .. + 15, dimension blocks of
+    // this wave; lane holds keys 16 kb + 4 g + r of dimension 16 db + n16
+    {
+      const u32x4_t ads = *reinterpret_cast<const u32x4_t*>(dst + (16 * kb + n16) * TS + 16 * g);
+      const u32x4_t ap = *reinterpret_cast<const u32x4_t*>(ptr + (16 * kb + n16) * TS + 16 * g);
+      int code[4];
+      float* rowp[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = rb + 16 * kb + 4 * g + r;  // list position
+        code[r] = j < r1 ? codes[j] : -1;
+        float* pool = j < nwin ? d_ori : d_cmp;
+        const int bs = j < nwin ? a.ori_block_size : a.cmp_block_size;
+        const int64_t bstr = j < nwin ? a.ori_block_stride : a.cmp_block_stride;
+        const int64_t rstr = j < nwin ? a.ori_row_stride : a.cmp_row_stride;
+        rowp[r] = nullptr;
+        if (code[r] >= 0 && pool) {
+          const int page = (int)((unsigned)code[r] / (unsigned)bs), off = code[r] - page * bs;
+          rowp[r] = pool + (size_t)page * bstr + (size_t)off * rstr;
+        }
+      }
+      for (int db = db0; db < db0 + NDB / 2; ++db) {
+        const int dim = 16 * db + n16;
+        const u32x4_t bq = *reinterpret_cast<const u32x4_t*>(qtr + dim * TS + 16 * g);
+        bw_f32x4 gk = bw_mfma<QT>(ads, bq, bw_f32x4{0.f, 0.f, 0.f, 0.f});
+        bw_f32x4 gv = bw_f32x4{0.f, 0.f, 0.f, 0.f};
+        if (16 * db < DV) {
+          const u32x4_t bo = *reinterpret_cast<const u32x4_t*>(otr + dim * TS + 16 * g);
+          gv = bw_mfma<QT>(ap, bo, gv);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (rowp[r]) atomicAdd(rowp[r] + dim, fmaf(gk[r], scale, gv[r]));
+      }
     }
   }
 }

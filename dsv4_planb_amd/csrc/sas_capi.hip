@@ -359,8 +359,8 @@ int sas_backward_workspace_size(const sas_params_t* p, size_t* bytes) {
 }
 
 int sas_backward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
-                 const void* dout, const float* dlse, float* dq, float* dsinks, void* ws,
-                 size_t ws_bytes, sas_stream_t stream) {
+                 const void* dout, const float* dlse, float* dq, float* dsinks, float* d_ori_kv,
+                 float* d_cmp_kv, void* ws, size_t ws_bytes, sas_stream_t stream) {
   int rc = sas_validate(p);
   if (rc) return rc;
   if ((rc = check_tensors(p, t))) return rc;
@@ -413,6 +413,21 @@ int sas_backward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* p
                      static_cast<const int*>(w.ncmp), static_cast<const float*>(t->lse),
                      static_cast<const float*>(dterm), plan, dq);
   if ((rc = launch_status())) return rc;
+  if (d_ori_kv || d_cmp_kv) {  // the KV pools' gradient (accumulated into the buffers)
+    const dim3 gkv(a.unit_cap * ((H + sas::DK_HEADS - 1) / sas::DK_HEADS));
+    typedef void (*dkv_fn_t)(SasFwdArgs, const uint16_t*, const uint16_t*, const uint64_t*,
+                             const int*, const int*, const float*, const float*, const int*,
+                             float*, float*);
+    dkv_fn_t kf = p->head_dim_qk == 576
+                      ? (f16 ? &sas::bwd_dkv_kernel<576, 1> : &sas::bwd_dkv_kernel<576, 0>)
+                      : (f16 ? &sas::bwd_dkv_kernel<512, 1> : &sas::bwd_dkv_kernel<512, 0>);
+    hipLaunchKernelGGL(kf, gkv, dim3(256), 0, s, a, static_cast<const uint16_t*>(t->q),
+                       static_cast<const uint16_t*>(dout), static_cast<const uint64_t*>(w.addr),
+                       static_cast<const int*>(w.rows), static_cast<const int*>(w.ncmp),
+                       static_cast<const float*>(t->lse), static_cast<const float*>(dterm), plan,
+                       d_ori_kv, p->scenario >= 2 ? d_cmp_kv : nullptr);
+    if ((rc = launch_status())) return rc;
+  }
   hipLaunchKernelGGL(sas::bwd_dsink_kernel, dim3((H + 3) / 4), dim3(256), 0, s, T, H,
                      static_cast<const float*>(sterm), dsinks);
   return launch_status();

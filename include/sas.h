@@ -164,20 +164,26 @@ int sas_forward_noalloc(const sas_params_t* p, const sas_tensors_t* t, const int
 int sas_attend_timed(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
                      void* workspace, size_t workspace_bytes, sas_stream_t stream,
                      void* start_event, void* stop_event);
-/* ---- backward (queries and sinks) ----
+/* ---- backward ----
  * No counterpart in the reference, which keeps the LSE for a backward it does not
  * have (api.py:32-35,176-184).  For a forward call with the same params, inputs
  * and plan whose results are in t->out and t->lse: dq [T, H, head_dim_qk] fp32 =
  * dL/dq and dsinks [H] fp32 = dL/dsinks for dout = dL/dout [T, H, head_dim_v] in
  * the query dtype.  The gradient of the one-shot sink softmax over the rows the
  * forward attends (FA-2 style: D = <dout, out>, dS = P (dP - D)).  16-bit KV only
- * (fp8 KV: SAS_ERR_NOT_IMPLEMENTED); no gradient for the KV pools.  dq rows of
- * split tokens are summed with fp32 atomics (their summation order is not fixed);
- * dsinks is deterministic.  workspace: sas_backward_workspace_size bytes. */
+ * (fp8 KV: SAS_ERR_NOT_IMPLEMENTED).  dq rows of split tokens are summed with fp32
+ * atomics (their summation order is not fixed); dsinks is deterministic.
+ * d_ori_kv / d_cmp_kv (each may be NULL): fp32 buffers laid out like ori_kv /
+ * cmp_kv (the params' block and row strides, in elements, over the same number of
+ * blocks) into which the pools' gradient is ADDED (dK over head_dim_qk, dV over the
+ * first head_dim_v dimensions; rows read as zeros get nothing): zero them first.
+ * Rows read by several tokens are summed with fp32 atomics (order not fixed).
+ * d_cmp_kv is ignored in scenario 1.  workspace: sas_backward_workspace_size bytes. */
 int sas_backward_workspace_size(const sas_params_t* p, size_t* bytes);
 int sas_backward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan,
                  const void* dout, const float* dlse /* [T, H] or NULL */, float* dq,
-                 float* dsinks, void* workspace, size_t workspace_bytes, sas_stream_t stream);
+                 float* dsinks, float* d_ori_kv /* or NULL */, float* d_cmp_kv /* or NULL */,
+                 void* workspace, size_t workspace_bytes, sas_stream_t stream);
 /* Debug: copy the resolved row-code lists of every token into rows (int32
  * [T, win_left + 1 (+ topk in scenarios 2, 3)]: the token's window pool rows, then
  * directly after them its compressed pool rows; -1 = a row read as zeros) and the
