@@ -135,15 +135,18 @@ class SasLaunch:
         _lib.check(lib.sas_backward_workspace_size(ctypes.byref(p), ctypes.byref(need)),
                    "sas_backward_workspace_size")
         ws = torch.empty(int(need.value), dtype=torch.uint8, device=dev)
+        def pool_grad(pool):
+            # laid out like the pool (same strides, so padded pools work) over a zeroed
+            # storage: the kernel adds into it, and never touches the padding
+            n = 1 + sum((d - 1) * st for d, st in zip(pool.shape, pool.stride()))
+            return torch.zeros(n, dtype=torch.float32, device=dev).as_strided(pool.shape,
+                                                                               pool.stride())
+
         d_ori = d_cmp = None
         if kv_grad:
-            # laid out like the pools (same strides, so padded pools work), zeroed:
-            # the kernel adds into them
-            d_ori = torch.empty_strided(self.ori_kv.shape, self.ori_kv.stride(),
-                                        dtype=torch.float32, device=dev).zero_()
+            d_ori = pool_grad(self.ori_kv)
             if p.scenario >= 2 and self.cmp_kv is not None:
-                d_cmp = torch.empty_strided(self.cmp_kv.shape, self.cmp_kv.stride(),
-                                            dtype=torch.float32, device=dev).zero_()
+                d_cmp = pool_grad(self.cmp_kv)
         rc = lib.sas_backward(ctypes.byref(p), ctypes.byref(self.tensors), _ptr(self.plan),
                               _ptr(g), _ptr(gl), _ptr(dq), _ptr(dsinks), _ptr(d_ori), _ptr(d_cmp),
                               _ptr(ws), ws.numel(), _stream_handle(dev))

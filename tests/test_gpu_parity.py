@@ -101,6 +101,18 @@ def _fp8_edges():
                                            dist="reference"), {}, "reference_fp8"),
     ("fp8_prefill", lambda: make_case(B=1, H=128, seq_kv=[1024], q_per_seq=256, scenario=3,
                                       K=512, kv_dtype="fp8e4m3", seed=28), {}, "baseline"),
+    # 4 cores: every token is one long unit, so most tiles run the steady-state
+    # schedule (softmax of tile i inside the chain of tile i+1), at d_qk 512 and 576
+    ("fp8_d512_long_units", lambda: make_case(B=2, H=128, D=512, seq_kv=[5000, 12000], q_per_seq=2,
+                                              scenario=3, K=1024, kv_dtype="fp8e4m3", seed=29),
+     {"core_num": 4}, "baseline"),
+    ("fp8_long_units", lambda: make_case(B=2, H=128, seq_kv=[9000, 3000], q_per_seq=2, scenario=3,
+                                         K=1024, kv_dtype="fp8e4m3", seed=30),
+     {"core_num": 4}, "baseline"),
+    ("fp8_fp16q_long_units", lambda: make_case(B=2, H=64, seq_kv=[9000, 3000], q_per_seq=2,
+                                               scenario=3, K=1024, q_dtype="fp16",
+                                               kv_dtype="fp8e4m3", seed=31),
+     {"core_num": 4}, "baseline"),
 ])
 def test_fp8_paths(name, build, extra, rule):
     c = build()
