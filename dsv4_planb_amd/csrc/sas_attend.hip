@@ -419,9 +419,9 @@ __device__ __forceinline__ bool attend_unit(
 
   // ---- S^T = K Q^T: the chain of KSTEPS accumulating MFMAs, K fragments three ahead ----
   // work(ks) runs right after step ks's MFMA issues (ks = -1: before the first one,
-  // while the first K fragments are in flight).  The loop hangs the previous tile's
-  // softmax and a later tile's DMA on it, so that VALU, SALU and DMA issue overlap
-  // the matrix core instead of following it.
+  // while the first K fragments are in flight; ks = KSTEPS: after the last one).
+  // The loop hangs the previous tile's softmax and a later tile's DMA on it, so that
+  // VALU, SALU and DMA issue overlap the matrix core instead of following it.
   auto kread = [&](const lds_u8* tl, int ks, uint32_t kr) -> u32x4_t {
     return ks < 32 ? lds_read_b128(tl + kofs[ks & 1] + 64 * (ks >> 1))
                    : lds_read_b128(tl + (kr ^ (32u * (uint32_t)(ks - 32))));
@@ -454,6 +454,9 @@ __device__ __forceinline__ bool attend_unit(
         work(ks);
         SB();
       }
+      // the steady-state fp8 softmax ends at step 32: past the last MFMA at d_qk 512
+      work(KSTEPS);
+      SB();
       return;
     }
     // the rope offset, formed per chain rather than kept across the loop

@@ -91,6 +91,18 @@ __device__ __forceinline__ int xcd_pair_slot(int k, int U) {
   return base + (r >> 1) + 8 * (r & 1);
 }
 
+// Workgroup of the unit emitted k-th when every unit starts in the first wave of
+// workgroups: consecutive runs of P = floor(U / 8) units go to one XCD (workgroups
+// x, x + 8, x + 16, ... all run on XCD x mod 8), so the splits of a token, which
+// each reload its query rows, and the MTP tokens of a sequence, which share their
+// window rows, meet in one L2.  The last U mod 8 keep their order.  A bijection on
+// [0, U).
+__device__ __forceinline__ int xcd_run_slot(int k, int U) {
+  const int P = U >> 3;
+  if (P == 0 || k >= 8 * P) return k;
+  return 8 * (k % P) + k / P;
+}
+
 __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
                                                        const int* __restrict__ q_prefix,
                                                        const int* __restrict__ act_q,
@@ -194,7 +206,9 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
   }
   const int U = scan_u[PLAN_NT - 1];
   int ub = scan_u[tid] - my_u, sb = scan_s[tid] - my_s, kb = scan_k[tid] - my_k;
-  const bool pair_xcd = (long long)a.T <= 4 * (long long)a.B;
+  const bool decode_like = (long long)a.T <= 4 * (long long)a.B;
+  // runs: every unit starts at once and some token is split (its units share Q rows)
+  const bool runs = U <= a.target && U > a.T;
   for (int t = t0; t < t1; ++t) {
     int* r = tok + (size_t)t * SAS_TOK_W;
     const int b = r[TK_B];
@@ -206,11 +220,12 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     if (splits > 1) ct = ((rows + splits - 1) / splits + SAS_TILE - 1) / SAS_TILE * SAS_TILE;
     for (int i = 0; i < splits; ++i) {
       // units are emitted in reverse order so the longest (latest prefill) tokens start
-      // first.  Decode-like plans (at most 4 query tokens per sequence) also put pairs of
-      // neighbouring units 8 workgroups apart: workgroups go to the 8 XCDs in turn, so
-      // the MTP tokens of a sequence, which share their window rows, share an XCD's L2.
+      // first.  Decode-like plans (at most 4 query tokens per sequence) also keep
+      // neighbouring units on one XCD: runs of U / 8 when all units start at once and
+      // tokens are split, else pairs 8 workgroups apart (workgroups go to the 8 XCDs
+      // in turn).
       const int k = U - 1 - (ub + i);
-      const int slot = pair_xcd ? xcd_pair_slot(k, U) : k;
+      const int slot = !decode_like ? k : runs ? xcd_run_slot(k, U) : xcd_pair_slot(k, U);
       if (slot < 0 || slot >= L.unit_cap) continue;  // (U <= unit_cap: flagged below if not)
       int* ur = units + (size_t)slot * SAS_UNIT_W;
       long long r0 = (long long)i * ct, r1 = r0 + ct < rows ? r0 + ct : rows;

@@ -471,6 +471,29 @@ def test_device_plan_keeps_uniform_decode_unsplit():
     print("\n[case] plan: uniform B=128 x 131072, 2 tokens", flush=True)
     units = _plan_units([2] * 128, [131072] * 128, 2048, 256)
     assert len(units) == 256 and (units[:, 3] == 0).all()
+    # the two MTP tokens of a sequence run on one XCD (workgroup id mod 8)
+    xcd = np.empty(256, np.int64)
+    xcd[units[:, 0]] = np.arange(256) % 8
+    assert (xcd[0::2] == xcd[1::2]).all()
+
+
+def test_device_plan_keeps_a_tokens_splits_on_one_xcd():
+    """A small decode batch (32 sequences, 1 query token, KV in [4096, 32768], top-k
+    512) splits every token over several units, all started at once: the units of a
+    token take workgroups of one XCD (id mod 8), except where a token straddles the
+    boundary between two XCDs' runs of U / 8 units (at most 7 tokens)."""
+    rng = np.random.default_rng(0)
+    kv = rng.integers(4096, 32769, size=32).tolist()
+    print("\n[case] plan: B=32 x [4096, 32768], 1 token, top-k 512", flush=True)
+    units = _plan_units([1] * 32, kv, 512, 256)
+    U = len(units)
+    assert U <= 256 and (units[:, 3] > 0).any()
+    xcds = {}
+    for slot, (t, _, _, _) in enumerate(units.tolist()):
+        xcds.setdefault(t, set()).add(slot % 8)
+    straddling = [t for t, s in xcds.items() if len(s) > 1]
+    assert len(xcds) == 32 and len(straddling) <= 7, straddling
+    assert all(len(s) <= 2 for s in xcds.values())
 
 
 def test_device_plan_fills_one_wave():
