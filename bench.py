@@ -260,8 +260,9 @@ def measure(wl, steps, warmup, core_num=256, settle_s=0.25):
     headline), (5) the per-call distribution of `steps` more replays, (6) the
     attention stage alone after a settle phase of its own: `steps` launches timed
     by their own dispatch events (`attend_kernel_us`, the roofline's kernel time)
-    and by events around them (`attend_us`), (7) the other stages and the eager
-    API call."""
+    and by events around them (`attend_us`), (7) the other stages, the forward
+    call launched eagerly through the C ABI (`eager_call_us`) and the eager API
+    call."""
     from dsv4_planb_amd import sparse_attn_sharedkv
     from dsv4_planb_amd.graph import SasGraph
 
@@ -298,6 +299,12 @@ def measure(wl, steps, warmup, core_num=256, settle_s=0.25):
         attend_us = _events_time(attend, steps, stream)
         resolve_us = _events_time(lambda: launch.run("resolve"), steps, stream)
         combine_us = _events_time(lambda: launch.run("combine"), steps, stream)
+        # the same forward call launched eagerly through the C ABI, back to back (the
+        # host runs ahead, so this is the device time without hipGraphLaunch's own
+        # cost per replay)
+        forward = lambda: launch.run("forward")  # noqa: E731
+        _settle(forward, settle_s, stream)
+        eager_call_us = _events_time(forward, steps, stream)
         plan_p = launch.params
         from dsv4_planb_amd.metadata import device_plan
         plan_us = _events_time(lambda: device_plan(plan_p, cu[:-1], cu[1:] - cu[:-1], wl["seqused"]),
@@ -317,8 +324,8 @@ def measure(wl, steps, warmup, core_num=256, settle_s=0.25):
         eager_us = (time.perf_counter() - t1) * 1e6 / steps
         graph.close()
     ok = bool(torch.isfinite(out.float()).all().item())
-    return dict(call_us=call_us, attend_us=attend_us, attend_kernel_us=attend_kernel_us,
-                resolve_us=resolve_us,
+    return dict(call_us=call_us, eager_call_us=eager_call_us, attend_us=attend_us,
+                attend_kernel_us=attend_kernel_us, resolve_us=resolve_us,
                 combine_us=combine_us, plan_us=plan_us, plan_host_us=plan_host_us,
                 eager_api_us=eager_us, finite=ok, call_dist_us=call_dist,
                 attend_dist_us=attend_dist, cold_call_us=[round(x, 1) for x in cold],
@@ -475,16 +482,17 @@ def cpu_baseline(name, n_seq, seed=0):
                 sample=f"{sample}; sample took {secs:.2f} s")
 
 
-def profile_attend(name, steps, dev, core_num=256):
+def profile_attend(name, steps, dev, core_num=256, stage="attend"):
     """Plan and resolve once, then launch only the attention stage `steps` times
-    (the kernel the roofline rates), for rocprofv3 counter runs."""
+    (the kernel the roofline rates), or the whole forward call (resolve,
+    attention, combine) with stage="forward", for rocprofv3 counter runs."""
     wl = make_workload(name, seed=0, dev=dev)
     _, launch, _, _ = build_call(wl, core_num)
     launch.run("resolve")
     for _ in range(steps):
-        launch.run("attend")
+        launch.run(stage)
     torch.cuda.synchronize()
-    print(json.dumps({"mode": "attend", "workload": name, "launches": steps,
+    print(json.dumps({"mode": stage, "workload": name, "launches": steps,
                       "alg_bytes": wl["alg_bytes"], "alg_flops": wl["alg_flops"]}))
 
 
@@ -583,9 +591,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-peaks", action="store_true",
                     help="skip the on-box MFMA / HBM peak probes")
-    ap.add_argument("--mode", default="bench", choices=["bench", "attend", "copy", "power"],
+    ap.add_argument("--mode", default="bench", choices=["bench", "attend", "forward", "copy", "power"],
                     help="bench: the JSON line; attend: only the attention stage of --workload, "
-                         "--steps launches (for counter runs); copy: a 1 GiB device copy, "
+                         "--steps launches (for counter runs); forward: the whole call (resolve, "
+                         "attention, combine), --steps times; copy: a 1 GiB device copy, "
                          "--steps times (calibrates the HBM byte counters); power: --stage back "
                          "to back for --secs with a power / clock sample")
     ap.add_argument("--stage", default="decode128k",
@@ -614,8 +623,8 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"mode": "copy", "bytes_per_copy": src.numel(), "copies": args.steps}))
         return
-    if args.mode == "attend":
-        profile_attend(args.workload, args.steps, dev)
+    if args.mode in ("attend", "forward"):
+        profile_attend(args.workload, args.steps, dev, stage=args.mode)
         return
     if args.mode == "power":
         power_mode(args.stage, args.secs, dev, compact=args.compact)
