@@ -482,17 +482,18 @@ def cpu_baseline(name, n_seq, seed=0):
                 sample=f"{sample}; sample took {secs:.2f} s")
 
 
-def profile_attend(name, steps, dev, core_num=256, stage="attend"):
+def profile_attend(name, steps, dev, core_num=256, stage="attend", compact=False):
     """Plan and resolve once, then launch only the attention stage `steps` times
     (the kernel the roofline rates), or the whole forward call (resolve,
-    attention, combine) with stage="forward", for rocprofv3 counter runs."""
-    wl = make_workload(name, seed=0, dev=dev)
+    attention, combine) with stage="forward", for rocprofv3 counter runs.
+    compact: the MALL-sized KV footprint of make_workload."""
+    wl = make_workload(name, seed=0, dev=dev, compact=compact)
     _, launch, _, _ = build_call(wl, core_num)
     launch.run("resolve")
     for _ in range(steps):
         launch.run(stage)
     torch.cuda.synchronize()
-    print(json.dumps({"mode": stage, "workload": name, "launches": steps,
+    print(json.dumps({"mode": stage, "workload": name, "compact": compact, "launches": steps,
                       "alg_bytes": wl["alg_bytes"], "alg_flops": wl["alg_flops"]}))
 
 
@@ -603,7 +604,8 @@ def main():
                     help="what --mode power runs")
     ap.add_argument("--secs", type=float, default=10.0, help="--mode power duration")
     ap.add_argument("--compact", action="store_true",
-                    help="--mode power: all sequences read the first sequence's KV pages")
+                    help="--mode power / attend / forward: all sequences read the first "
+                         "sequence's KV pages")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -624,7 +626,7 @@ def main():
         print(json.dumps({"mode": "copy", "bytes_per_copy": src.numel(), "copies": args.steps}))
         return
     if args.mode in ("attend", "forward"):
-        profile_attend(args.workload, args.steps, dev, stage=args.mode)
+        profile_attend(args.workload, args.steps, dev, stage=args.mode, compact=args.compact)
         return
     if args.mode == "power":
         power_mode(args.stage, args.secs, dev, compact=args.compact)
