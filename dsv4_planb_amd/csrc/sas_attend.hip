@@ -185,8 +185,7 @@ constexpr int gather_cpol() { return STREAM ? 2 : 0; }  // 2: the NT bit of the 
 template <int DQK, int QT, bool STREAM, bool KV8, bool REDO>
 __device__ __forceinline__ bool attend_unit(
     int u, AttendLds<DQK, KV8>& sm, const SasFwdArgs& a, const uint16_t* __restrict__ q,
-    const uint64_t* __restrict__ addr_list, const float* __restrict__ scale_list,
-    const int* __restrict__ ncmp,
+    const uint64_t* addr_list, const float* scale_list, int ncmp_t,
     const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
     float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml, float& m_obs) {
   constexpr int DV = 512;
@@ -230,7 +229,7 @@ __device__ __forceinline__ bool attend_unit(
   const int nwin = min(tk[TK_NWIN], a.win_left + 1);
   const int splits = tk[TK_SPLITS], wsbase = tk[TK_WSBASE];
   const int r0 = ur[1];
-  const int r1 = min(min(ur[2], nwin + ncmp[t]), a.list_stride);
+  const int r1 = min(min(ur[2], nwin + ncmp_t), a.list_stride);
   const int ntiles = r1 > r0 ? (r1 - r0 + TILE - 1) / TILE : 0;
   // row addresses of this unit's list (pool addresses; -1 codes read the zero row)
   const uint64_t* alist = addr_list + (size_t)t * a.list_stride + r0;
@@ -365,7 +364,10 @@ __device__ __forceinline__ bool attend_unit(
   };
   auto load_addrs = [&](int i) -> RowAddrs {
     const int il = min(i, ntiles - 1);  // dead tiles (i >= ntiles) read zeros
-    return fix_tail(*reinterpret_cast<const RowAddrs*>(alist + il * TILE + 8 * wu), i);
+    // through the constant address space: a scalar load, whatever stores the kernel
+    // made before (its DMA waits count vector-memory instructions)
+    typedef __attribute__((address_space(4))) const RowAddrs c_RowAddrs;
+    return fix_tail(*(c_RowAddrs*)(uintptr_t)(alist + il * TILE + 8 * wu), i);
   };
   // One row through a raw buffer resource based at the row (loads directly into
   // LDS, never the FLAT form: an outstanding FLAT load that writes LDS makes every
@@ -981,17 +983,22 @@ __device__ __forceinline__ bool attend_unit(
 
 namespace sas {
 
-// One workgroup per work unit.
+// One workgroup per work unit.  rs.addr set: the resolver stage did not run, and
+// each unit first resolves its own rows (lists, scales, codes) into the workspace.
 template <int DQK, int QT, bool STREAM, bool KV8>
 __global__ __launch_bounds__(256, 1) void attend_kernel(
-    SasFwdArgs a, const uint16_t* __restrict__ q, const uint64_t* __restrict__ addr_list,
-    const float* __restrict__ scale_list, const int* __restrict__ ncmp,
+    SasFwdArgs a, const uint16_t* __restrict__ q, const uint64_t* addr_list,
+    const float* scale_list, const int* __restrict__ ncmp,
     const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
-    float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+    float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml,
+    SasResolveArgs rs) {
   __shared__ __attribute__((aligned(16))) AttendLds<DQK, KV8> sm;
+  static_assert(sizeof(RsShared) <= sizeof(sm.tiles), "the resolution borrows the tile ring");
   const int u = blockIdx.x;
-  if (!plan_matches(plan, a)) {  // a plan built for other arguments: zeros (the resolver
-    if (u < a.T) {               // flagged the call in the workspace status word)
+  const bool plan_ok = plan_matches(plan, a);
+  if (rs.addr && u == 0 && threadIdx.x == 0) *rs.status = plan_ok ? SAS_OK : SAS_ERR_PLAN;
+  if (!plan_ok) {  // a plan built for other arguments: zeros (the call's status word
+    if (u < a.T) { // says so)
       for (int i = threadIdx.x; i < a.H * 512 / 8; i += 256)
         reinterpret_cast<u32x4_t*>(out + (size_t)u * a.H * 512)[i] = u32x4_t{0, 0, 0, 0};
       if (lse)
@@ -1000,11 +1007,31 @@ __global__ __launch_bounds__(256, 1) void attend_kernel(
     return;
   }
   if (u >= plan[PH_UNITS]) return;
+  const int* ur = plan + SAS_PLAN_HDR + (size_t)SAS_TOK_W * a.T + (size_t)u * SAS_UNIT_W;
+  const int t = ur[0];
+  int ncmp_t;  // the token's compressed row count (at least what this unit needs)
+  if (rs.addr) {
+    const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
+    const int split = ur[3];
+    ncmp_t = split < 0 ? 0
+                       : resolve_rows(a, tk, true, t, ur[1], min(ur[2], a.list_stride),
+                                      *reinterpret_cast<RsShared*>(sm.tiles), rs);
+    // The token's last unit scans its list to the end: its count is exact.
+    if (rs.ncmp && threadIdx.x == 0 && (split < 0 || split == tk[TK_SPLITS] - 1)) rs.ncmp[t] = ncmp_t;
+    // Every wave's stores have reached L2 before any wave reads the lists back
+    // (scalar loads and the scale DMA), and every wave is done with the borrowed LDS.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  } else {
+    ncmp_t = ncmp[t];
+  }
+  // The lists are read through pointers the compiler cannot trace to the stores
+  // above, so none of those loads moves before the barrier.
+  asm volatile("" : "+s"(addr_list), "+s"(scale_list));
   float m_obs = 0.f;
-  if (attend_unit<DQK, QT, STREAM, KV8, false>(u, sm, a, q, addr_list, scale_list, ncmp, sinks, plan,
+  if (attend_unit<DQK, QT, STREAM, KV8, false>(u, sm, a, q, addr_list, scale_list, ncmp_t, sinks, plan,
                                                out, lse, ws_o, ws_ml, m_obs)) {
     lds_barrier();  // every wave is done with the ring before the redo refills it
-    attend_unit<DQK, QT, STREAM, KV8, true>(u, sm, a, q, addr_list, scale_list, ncmp, sinks, plan,
+    attend_unit<DQK, QT, STREAM, KV8, true>(u, sm, a, q, addr_list, scale_list, ncmp_t, sinks, plan,
                                             out, lse, ws_o, ws_ml, m_obs);
   }
 }

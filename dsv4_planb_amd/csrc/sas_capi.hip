@@ -129,7 +129,27 @@ int carve(const sas_params_t* p, void* ws, size_t ws_bytes, int target, Ws* out)
 }
 
 typedef void (*attend_fn_t)(SasFwdArgs, const uint16_t*, const uint64_t*, const float*,
-                            const int*, const float*, const int*, uint16_t*, float*, float*, float*);
+                            const int*, const float*, const int*, uint16_t*, float*, float*, float*,
+                            sas::SasResolveArgs);
+
+// Resolution's inputs and outputs in the workspace.
+sas::SasResolveArgs resolve_args(const sas_params_t* p, const sas_tensors_t* t, const Ws& w) {
+  sas::SasResolveArgs r;
+  r.status = w.status;
+  r.ori_bt = t->ori_block_table;
+  r.idx = t->cmp_sparse_indices;
+  r.cmp_bt = t->cmp_block_table;
+  r.rows = w.rows;
+  r.ncmp = w.ncmp;
+  r.addr = w.addr;
+  r.ori_kv = static_cast<const uint8_t*>(t->ori_kv);
+  r.cmp_kv = static_cast<const uint8_t*>(t->cmp_kv);
+  r.esz = p->kv_dtype == SAS_DT_FP8E4M3 ? 1 : 2;
+  r.ori_scale = t->ori_kv_scale;
+  r.cmp_scale = t->cmp_kv_scale;
+  r.scale = w.scale;
+  return r;
+}
 
 template <int DQK, bool NT, bool KV8>
 attend_fn_t attend_ptr(bool f16) {
@@ -154,6 +174,24 @@ attend_fn_t pick_attend(const sas_params_t* p) {
 }
 
 int launch_status() { return hipGetLastError() == hipSuccess ? SAS_OK : SAS_ERR_LAUNCH; }
+
+// The attention kernel over the plan's units.  resolve: each unit first resolves
+// its own rows (the resolver stage is then not launched).  With events, the
+// dispatch itself records its start and end into them.
+int launch_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, const Ws& w,
+                  int target, sas_stream_t stream, void* start_event, void* stop_event,
+                  bool resolve) {
+  const SasFwdArgs a = fwd_args(p, target);
+  sas::SasResolveArgs r = resolve_args(p, t, w);
+  if (!resolve) r.addr = nullptr;
+  hipExtLaunchKernelGGL(pick_attend(p), dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream,
+                        (hipEvent_t)start_event, (hipEvent_t)stop_event, 0, a,
+                        static_cast<const uint16_t*>(t->q), static_cast<const uint64_t*>(w.addr),
+                        static_cast<const float*>(w.scale), static_cast<const int*>(w.ncmp),
+                        t->sinks, static_cast<const int*>(plan), static_cast<uint16_t*>(t->out),
+                        t->lse, w.o, w.ml, r);
+  return launch_status();
+}
 
 }  // namespace
 
@@ -269,10 +307,7 @@ int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   if (!plan) plan = w.plan;
   if (p->total_tokens == 0) return SAS_OK;
   hipLaunchKernelGGL(sas::resolve_kernel, dim3(p->total_tokens), dim3(sas::RS_NT), 0,
-                     (hipStream_t)stream, fwd_args(p, target), plan, w.status, t->ori_block_table,
-                     t->cmp_sparse_indices, t->cmp_block_table, w.rows, w.ncmp, w.addr,
-                     static_cast<const uint8_t*>(t->ori_kv), static_cast<const uint8_t*>(t->cmp_kv),
-                     p->kv_dtype == SAS_DT_FP8E4M3 ? 1 : 2, t->ori_kv_scale, t->cmp_kv_scale, w.scale);
+                     (hipStream_t)stream, fwd_args(p, target), plan, resolve_args(p, t, w));
   return launch_status();
 }
 
@@ -286,15 +321,7 @@ int sas_attend_timed(const sas_params_t* p, const sas_tensors_t* t, const int32_
   if ((rc = carve(p, ws, ws_bytes, target, &w))) return rc;
   if (!plan) plan = w.plan;
   if (p->total_tokens == 0) return SAS_OK;
-  const SasFwdArgs a = fwd_args(p, target);
-  // with events: the dispatch itself records its start and end into them
-  hipExtLaunchKernelGGL(pick_attend(p), dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream,
-                        (hipEvent_t)start_event, (hipEvent_t)stop_event, 0, a,
-                        static_cast<const uint16_t*>(t->q), static_cast<const uint64_t*>(w.addr),
-                        static_cast<const float*>(w.scale), static_cast<const int*>(w.ncmp),
-                        t->sinks, static_cast<const int*>(plan), static_cast<uint16_t*>(t->out),
-                        t->lse, w.o, w.ml);
-  return launch_status();
+  return launch_attend(p, t, plan, w, target, stream, start_event, stop_event, false);
 }
 
 int sas_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
@@ -342,8 +369,16 @@ int sas_forward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
     if ((rc = launch_status())) return rc;
     plan = w.plan;
   }
-  if ((rc = sas_resolve(p, t, plan, ws, ws_bytes, stream))) return rc;
-  if ((rc = sas_attend(p, t, plan, ws, ws_bytes, stream))) return rc;
+  // At most as many tokens as target units: every unit starts in the first wave
+  // of workgroups, and each resolves its own rows before its first DMA (one
+  // launch fewer).  Otherwise units queue behind each other on a CU, and the
+  // resolver runs first as a stage of its own.
+  if ((int64_t)p->total_tokens <= (int64_t)target) {
+    if ((rc = launch_attend(p, t, plan, w, target, stream, nullptr, nullptr, true))) return rc;
+  } else {
+    if ((rc = sas_resolve(p, t, plan, ws, ws_bytes, stream))) return rc;
+    if ((rc = sas_attend(p, t, plan, ws, ws_bytes, stream))) return rc;
+  }
   return sas_combine(p, t, plan, ws, ws_bytes, stream);
 }
 
@@ -442,10 +477,13 @@ int sas_debug_rows(const sas_params_t* p, const void* ws, int32_t* rows, int32_t
   const SasWsLayout W = sas_ws_layout(p->total_tokens, K, p->num_heads_q, p->head_dim_v,
                                       target_units(p), p->scenario, p->ori_win_left,
                                       p->kv_dtype == SAS_DT_FP8E4M3);
+  // the workspace lists sit at the tile-rounded stride; rows gets the capacity
   const size_t stride = (size_t)sas_row_list_stride(p->ori_win_left, K, p->scenario);
+  const size_t cap = (size_t)sas_row_list_cap(p->ori_win_left, K, p->scenario);
   const char* base = static_cast<const char*>(ws);
-  if (hipMemcpyAsync(rows, base + W.off_rows, (size_t)p->total_tokens * stride * 4,
-                     hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)
+  if (p->total_tokens > 0 &&
+      hipMemcpy2DAsync(rows, cap * 4, base + W.off_rows, stride * 4, cap * 4, (size_t)p->total_tokens,
+                       hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)
     return SAS_ERR_LAUNCH;
   if (hipMemcpyAsync(counts, base + W.off_ncmp, (size_t)p->total_tokens * 4,
                      hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)

@@ -71,8 +71,15 @@ SAS_HD static inline size_t sas_align256(size_t x) { return (x + 255) & ~(size_t
 // Row-code list of one token: its window rows, then directly after them its
 // compressed rows (scenario 3: the resolved top-k; scenario 2: every causally
 // valid row, up to K of them).  Capacity: win_left + 1 + K slots.
-SAS_HD static inline int64_t sas_row_list_stride(int64_t win_left, int64_t K, int scenario) {
+SAS_HD static inline int64_t sas_row_list_cap(int64_t win_left, int64_t K, int scenario) {
   return win_left + 1 + (scenario >= 2 ? K : 0);
+}
+// Distance between two tokens' lists: the capacity rounded up to whole tiles.  Work
+// units of different tokens resolve and read their lists concurrently; so no 64-B
+// line of the code, address or scale lists holds rows of two tokens, and a unit's
+// last tile, read whole, stays inside its own token's list.
+SAS_HD static inline int64_t sas_row_list_stride(int64_t win_left, int64_t K, int scenario) {
+  return (sas_row_list_cap(win_left, K, scenario) + SAS_TILE - 1) / SAS_TILE * SAS_TILE;
 }
 
 SAS_HD static inline SasWsLayout sas_ws_layout(int64_t T, int64_t K, int64_t H, int64_t Dv,

@@ -297,12 +297,8 @@ __device__ __forceinline__ int paged_code(const int* __restrict__ bt_row, int ta
   return (page < 0 || page >= block_num) ? -1 : page * block_size + (pos - blk * block_size);
 }
 
-// One workgroup (256 threads) per token.  The first min(K, thr) index slots are
-// taken in passes of RS_PER slabs of RS_NT slots; thread i owns slot i of every
-// slab, so each load and store instruction of a wave covers 64 consecutive slots.
-// The first -1 (a block-wide minimum) ends the list, ids outside [0, thr) are
-// skipped, and the survivors keep their slot order: a wave ranks its survivors of
-// a slab with one ballot, and the per-(slab, wave) counts go through LDS.
+// A token is resolved by one workgroup of RS_NT threads (the resolver's own, or
+// the attention workgroup of one of its units).
 constexpr int RS_NT = 256;
 constexpr int RS_WAVES = RS_NT / 64;
 
@@ -316,27 +312,47 @@ constexpr int RS_PER = 8;  // slabs per pass (index slots per thread and pass)
 
 constexpr int RS_CBT_LDS = 4096;  // compressed block-table entries staged in LDS
 
-__global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int* __restrict__ plan,
-                                                        int* __restrict__ status,
-                                                        const int* __restrict__ ori_bt,
-                                                        const int* __restrict__ idx,
-                                                        const int* __restrict__ cmp_bt,
-                                                        int* __restrict__ rows_out,
-                                                        int* __restrict__ ncmp_out,
-                                                        uint64_t* __restrict__ addr_out,
-                                                        const uint8_t* __restrict__ ori_kv,
-                                                        const uint8_t* __restrict__ cmp_kv,
-                                                        int esz,
-                                                        const float* __restrict__ ori_scale,
-                                                        const float* __restrict__ cmp_scale,
-                                                        float* __restrict__ scale_out) {
-  __shared__ int s_wmin[RS_WAVES];
-  __shared__ int s_cnt[RS_PER][RS_WAVES];
-  __shared__ int s_cbt[RS_CBT_LDS];
-  const int t = blockIdx.x;
+// LDS of one token's resolution (the attention kernel lends it the start of its
+// tile ring, which is empty until the unit's first DMA).
+struct RsShared {
+  int wmin[RS_WAVES];
+  int cnt[RS_PER][RS_WAVES];
+  int cbt[RS_CBT_LDS];
+};
+
+// Inputs and outputs of row resolution.
+struct SasResolveArgs {
+  int* status;            // the call's status word (the plan check)
+  const int* ori_bt;
+  const int* idx;
+  const int* cmp_bt;
+  int* rows;              // row codes (nullptr: not written)
+  int* ncmp;              // per-token compressed row counts (nullptr: not written)
+  uint64_t* addr;         // row addresses (nullptr: the rows were resolved beforehand)
+  const uint8_t* ori_kv;
+  const uint8_t* cmp_kv;
+  int esz;                // bytes per KV element
+  const float* ori_scale;
+  const float* cmp_scale;
+  float* scale;           // fp8: s, then (T * list_stride on) 1 / s; nullptr for 16-bit KV
+};
+
+// List positions [lo, hi) of token t (its window rows, then its compressed rows)
+// resolved into codes, pool addresses and (fp8) scales, by the workgroup's RS_NT
+// threads.  The first min(K, thr) index slots are taken in passes of RS_PER slabs
+// of RS_NT slots; thread i owns slot i of every slab, so each load and store
+// instruction of a wave covers 64 consecutive slots.  The first -1 (a block-wide
+// minimum) ends the list, ids outside [0, thr) are skipped, and the survivors keep
+// their slot order: a wave ranks its survivors of a slab with one ballot, and the
+// per-(slab, wave) counts go through LDS.  Returns the token's compressed row count
+// when the scan reached the list's end, else a number >= hi - nwin (the scan stops
+// after the pass that resolves position hi - 1).  A token no batch owns, or a
+// refused plan, resolves to nothing.
+__device__ int resolve_rows(const SasFwdArgs& a, const int* tk, bool plan_ok, int t, int lo, int hi,
+                            RsShared& sh, const SasResolveArgs& r) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
-  const int* ir = idx + (size_t)t * a.K;
+  const int* ir = r.idx + (size_t)t * a.K;
   // This thread's slot of every slab of the pass at c0, all loaded before any is
   // used (-2: at or past the bound).
   auto load_slots = [&](int (&v)[RS_PER], int c0, int bound) {
@@ -350,69 +366,55 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
   // first pass of its index slots.
   int v0[RS_PER];
   if (a.scenario == 3) load_slots(v0, 0, a.K);
-  // A plan built for other arguments is refused: the call's status word says so,
-  // every token resolves to no rows, and the attention kernel writes zeros.
-  const bool plan_ok = plan_matches(plan, a);
-  if (t == 0 && tid == 0) *status = plan_ok ? SAS_OK : SAS_ERR_PLAN;
-  const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
   const int b = plan_ok ? tk[TK_B] : -1;
-  if (b < 0 || b >= a.B) {
-    if (tid == 0) ncmp_out[t] = 0;
-    return;
-  }
-  int* out = rows_out + (size_t)t * a.list_stride;
-  uint64_t* aout = addr_out + (size_t)t * a.list_stride;
+  if (b < 0 || b >= a.B) return 0;
+  int* out = r.rows ? r.rows + (size_t)t * a.list_stride : nullptr;
+  uint64_t* aout = r.addr + (size_t)t * a.list_stride;
   // fp8 KV: each row's dequantisation scale s and 1 / s beside its address (a -1
   // code reads the zero row: s = 1, so that its P counts in the output normaliser
   // as a zero row of a 16-bit pool does)
-  float* sout = scale_out ? scale_out + (size_t)t * a.list_stride : nullptr;
+  float* sout = r.scale ? r.scale + (size_t)t * a.list_stride : nullptr;
   const size_t inv_off = (size_t)a.T * a.list_stride;  // the 1 / s list follows the s list
-  auto put_scale = [&](int r, int code, const float* __restrict__ sc) {
-    const float s = code < 0 ? 1.f : sc[code];
-    sout[r] = s;
-    sout[inv_off + r] = s != 0.f ? 1.f / s : 0.f;
+  auto put_scale = [&](int p, float s) {
+    sout[p] = s;
+    sout[inv_off + p] = s != 0.f ? 1.f / s : 0.f;
   };
   const int nwin = min(tk[TK_NWIN], a.win_left + 1), winlo = tk[TK_WINLO];
   // Second: the window's block-table entries and the batch's compressed block-table
   // row, staged in LDS so the per-id page lookups below stay on chip.
-  const int* cbt_g = cmp_bt + (size_t)b * a.cmp_table_len;
+  const int* cbt_g = r.cmp_bt + (size_t)b * a.cmp_table_len;
   const bool cbt_lds = a.scenario >= 2 && a.cmp_table_len <= RS_CBT_LDS;
   if (cbt_lds)
-    for (int i = tid; i < a.cmp_table_len; i += RS_NT) s_cbt[i] = cbt_g[i];
-  const int* obt = ori_bt + (size_t)b * a.ori_table_len;
-  for (int r = tid; r < nwin; r += RS_NT) {
-    const int code = paged_code(obt, a.ori_table_len, a.ori_block_size, a.ori_block_num, winlo + r);
-    out[r] = code;
-    aout[r] = code_addr(code, ori_kv, a.ori_block_size, a.ori_block_stride, a.ori_row_stride, esz);
-    if (sout) put_scale(r, code, ori_scale);
+    for (int i = tid; i < a.cmp_table_len; i += RS_NT) sh.cbt[i] = cbt_g[i];
+  const int* obt = r.ori_bt + (size_t)b * a.ori_table_len;
+  for (int p = lo + tid; p < min(hi, nwin); p += RS_NT) {
+    const int code = paged_code(obt, a.ori_table_len, a.ori_block_size, a.ori_block_num, winlo + p);
+    if (out) out[p] = code;
+    aout[p] = code_addr(code, r.ori_kv, a.ori_block_size, a.ori_block_stride, a.ori_row_stride, r.esz);
+    if (sout) put_scale(p, code < 0 ? 1.f : r.ori_scale[code]);
   }
-  aout += nwin;
-  if (sout) sout += nwin;
-  if (a.scenario == 1) {
-    if (tid == 0) ncmp_out[t] = 0;
-    return;
-  }
-  rs_barrier();  // s_cbt
-  const int* cbt = cbt_lds ? s_cbt : cbt_g;
-  out += nwin;  // compressed codes follow the window codes
+  if (a.scenario == 1) return 0;
+  rs_barrier();  // sh.cbt
+  const int* cbt = cbt_lds ? sh.cbt : cbt_g;
   const int thr = floor_div(tk[TK_SG] + 1, a.cmp_ratio);
+  // compressed rows j sit at list position nwin + j; [lo, hi) holds j in [jlo, jhi)
+  const int jlo = max(lo - nwin, 0), jhi = hi - nwin;
   if (a.scenario == 2) {  // golden.py:146-150: every compressed row below thr
     const int n = max(min(thr, a.K), 0);
-    for (int j = tid; j < n; j += RS_NT) {
+    for (int j = jlo + tid; j < min(n, jhi); j += RS_NT) {
       const int code = paged_code(cbt, a.cmp_table_len, a.cmp_block_size, a.cmp_block_num, j);
-      out[j] = code;
-      aout[j] = code_addr(code, cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
-      if (sout) put_scale(j, code, cmp_scale);
+      if (out) out[nwin + j] = code;
+      aout[nwin + j] = code_addr(code, r.cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, r.esz);
+      if (sout) put_scale(nwin + j, code < 0 ? 1.f : r.cmp_scale[code]);
     }
-    if (tid == 0) ncmp_out[t] = n;
-    return;
+    return n;
   }
   const int limit = max(min(a.K, thr), 0);  // golden.py:48
   // Passes of RS_PER slabs of RS_NT slots; the terminator, the survivors and their
   // slot-order positions come from ballots and two LDS exchanges per pass.
-  int emitted = 0;  // compressed rows written so far (block-uniform)
+  int emitted = 0;  // compressed rows found so far (block-uniform)
   const uint64_t below = (1ull << lane) - 1;  // lanes ranked before this one
-  for (int c0 = 0; c0 < limit; c0 += RS_NT * RS_PER) {
+  for (int c0 = 0; c0 < limit && emitted < jhi; c0 += RS_NT * RS_PER) {
     int v[RS_PER];
     if (c0 == 0) {
 #pragma unroll
@@ -429,11 +431,11 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
       const uint64_t m = __ballot(v[k] == -1);
       if (m) first = c0 + k * RS_NT + w * 64 + (int)__builtin_ctzll(m);
     }
-    if (lane == 0) s_wmin[w] = first;
+    if (lane == 0) sh.wmin[w] = first;
     rs_barrier();
-    int term = s_wmin[0];
+    int term = sh.wmin[0];
 #pragma unroll
-    for (int j = 1; j < RS_WAVES; ++j) term = min(term, s_wmin[j]);
+    for (int j = 1; j < RS_WAVES; ++j) term = min(term, sh.wmin[j]);
     // golden.py:58-59: ids at or beyond thr are skipped (other negatives too).
     // Survivors of slab k are ranked within the wave by a ballot; the counts of
     // every (slab, wave) give each wave's base position.
@@ -444,7 +446,7 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
       keep[k] = c0 + k * RS_NT + tid < term && v[k] >= 0 && v[k] < thr;
       const uint64_t m = __ballot(keep[k]);
       rank[k] = __popcll(m & below);
-      if (lane == 0) s_cnt[k][w] = __popcll(m);
+      if (lane == 0) sh.cnt[k][w] = __popcll(m);
     }
     rs_barrier();
     int pos[RS_PER];
@@ -454,12 +456,13 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
       int before = 0, slab = 0;
 #pragma unroll
       for (int j = 0; j < RS_WAVES; ++j) {
-        const int c = s_cnt[k][j];
+        const int c = sh.cnt[k][j];
         before += j < w ? c : 0;
         slab += c;
       }
       pos[k] = total + before + rank[k];
       total += slab;
+      keep[k] = keep[k] && pos[k] >= jlo && pos[k] < jhi;  // inside [lo, hi)
     }
     // The page lookups of the pass, then its codes, then every scale load, then the
     // stores: each load waits only for what it depends on (the block-table row is
@@ -472,7 +475,7 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     }
     if (cbt_lds) {
 #pragma unroll
-      for (int k = 0; k < RS_PER; ++k) page[k] = blk[k] >= 0 ? s_cbt[blk[k]] : -1;
+      for (int k = 0; k < RS_PER; ++k) page[k] = blk[k] >= 0 ? sh.cbt[blk[k]] : -1;
     } else {
 #pragma unroll
       for (int k = 0; k < RS_PER; ++k) page[k] = blk[k] >= 0 ? cbt_g[blk[k]] : -1;
@@ -485,23 +488,35 @@ __global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int*
     float sc[RS_PER];
     if (sout) {
 #pragma unroll
-      for (int k = 0; k < RS_PER; ++k) sc[k] = code[k] >= 0 ? cmp_scale[code[k]] : 1.f;
+      for (int k = 0; k < RS_PER; ++k) sc[k] = code[k] >= 0 ? r.cmp_scale[code[k]] : 1.f;
     }
 #pragma unroll
     for (int k = 0; k < RS_PER; ++k)
       if (keep[k]) {
-        out[pos[k]] = code[k];
-        if (sout) {
-          sout[pos[k]] = sc[k];
-          sout[inv_off + pos[k]] = sc[k] != 0.f ? 1.f / sc[k] : 0.f;
-        }
-        aout[pos[k]] = code_addr(code[k], cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, esz);
+        const int p = nwin + pos[k];
+        if (out) out[p] = code[k];
+        if (sout) put_scale(p, sc[k]);
+        aout[p] = code_addr(code[k], r.cmp_kv, a.cmp_block_size, a.cmp_block_stride, a.cmp_row_stride, r.esz);
       }
     emitted = total;
     if (term < limit) break;  // the list ended in this pass
-    rs_barrier();          // s_wmin / s_cnt are rewritten by the next pass
+    rs_barrier();          // wmin / cnt are rewritten by the next pass
   }
-  if (tid == 0) ncmp_out[t] = emitted;
+  return emitted;
+}
+
+// One workgroup (RS_NT threads) per token: its whole list.
+__global__ __launch_bounds__(RS_NT) void resolve_kernel(SasFwdArgs a, const int* __restrict__ plan,
+                                                        SasResolveArgs r) {
+  __shared__ RsShared sh;
+  const int t = blockIdx.x;
+  // A plan built for other arguments is refused: the call's status word says so,
+  // every token resolves to no rows, and the attention kernel writes zeros.
+  const bool plan_ok = plan_matches(plan, a);
+  if (t == 0 && threadIdx.x == 0) *r.status = plan_ok ? SAS_OK : SAS_ERR_PLAN;
+  const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
+  const int n = resolve_rows(a, tk, plan_ok, t, 0, a.list_stride, sh, r);
+  if (threadIdx.x == 0 && r.ncmp) r.ncmp[t] = n;
 }
 
 // ===========================================================================

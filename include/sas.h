@@ -126,7 +126,10 @@ int sas_target_units(const sas_params_t* p, int32_t* units);
 int sas_plan(const sas_params_t* p, const int32_t* q_prefix, const int32_t* act_q_lens,
              const int32_t* seqused_kv, int32_t* plan, size_t plan_n_int32, sas_stream_t stream);
 /* Full forward: (plan if plan == NULL) -> index resolution -> attention ->
- * split combine.  plan may be a buffer filled by sas_plan for the same params
+ * split combine.  With at most as many tokens as balance-target units, every
+ * work unit resolves its own rows at the start of the attention kernel instead
+ * of a resolution stage of its own (same lists, codes and counts in the
+ * workspace).  plan may be a buffer filled by sas_plan for the same params
  * and lengths.  The plan's header records the arguments it was built for (token
  * and batch counts, scenario, window, ratio, top-k, balance target); the kernels
  * refuse a plan whose record differs from the call: the outputs are written as
