@@ -38,7 +38,9 @@ enum { TK_B = 0, TK_S, TK_SG, TK_NWIN, TK_WINLO, TK_NCMPMAX, TK_SPLITS, TK_WSBAS
 
 struct SasPlanLayout {
   int64_t T, target, unit_cap, split_cap;
-  int64_t off_tok, off_units, off_split_tokens, total;  // int32 offsets
+  // int32 offsets: token records, units, split tokens, and per split token its
+  // (split count, first workspace slot)
+  int64_t off_tok, off_units, off_split_tokens, off_split_meta, total;
 };
 
 SAS_HD static inline SasPlanLayout sas_plan_layout(int64_t T, int64_t target) {
@@ -50,7 +52,8 @@ SAS_HD static inline SasPlanLayout sas_plan_layout(int64_t T, int64_t target) {
   L.off_tok = SAS_PLAN_HDR;
   L.off_units = L.off_tok + SAS_TOK_W * T;
   L.off_split_tokens = L.off_units + SAS_UNIT_W * L.unit_cap;
-  L.total = L.off_split_tokens + L.split_cap;
+  L.off_split_meta = L.off_split_tokens + L.split_cap;
+  L.total = L.off_split_meta + 2 * L.split_cap;
   // A plan is never SAS_META_SIZE (1024) entries long, so a caller-supplied table
   // is told apart from the reference's int32[1024] metadata by its size alone.
   if (L.total == SAS_META_SIZE) L.total += 1;

@@ -115,6 +115,7 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
   int* tok = plan + L.off_tok;
   int* units = plan + L.off_units;
   int* stoks = plan + L.off_split_tokens;
+  int* smeta = plan + L.off_split_meta;
   const int per = (a.T + PLAN_NT - 1) / PLAN_NT;
   const int t0 = min(a.T, tid * per), t1 = min(a.T, t0 + per);
 
@@ -236,7 +237,11 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     }
     ub += splits;
     if (splits > 1) {
-      if (kb < L.split_cap) stoks[kb] = t;
+      if (kb < L.split_cap) {
+        stoks[kb] = t;
+        smeta[2 * kb] = splits;
+        smeta[2 * kb + 1] = sb;
+      }
       ++kb;
       sb += splits;
     }
@@ -603,7 +608,23 @@ __device__ __forceinline__ void combine_head(int t, int h, int H, int S, int bas
   auto record = [&](int s0) {
     return s0 + lane < S ? ml[(size_t)(base + s0 + lane) * H + h] : make_float4(-INFINITY, 0.f, 0.f, 0.f);
   };
+  // partial rows s0 + j0 .. s0 + j0 + COMBINE_BATCH - 1 (clamped to the last one, n rows
+  // in the chunk at s0)
+  auto load_batch = [&](float4 (&v)[COMBINE_BATCH][2], int s0, int j0, int n) {
+#pragma unroll
+    for (int j = 0; j < COMBINE_BATCH; ++j) {
+      const int jj = min(j0 + j, n - 1);
+      const float4* src =
+          reinterpret_cast<const float4*>(ws_o + ((size_t)(base + s0 + jj) * H + h) * DV) + 2 * lane;
+      v[j][0] = src[0];
+      v[j][1] = src[1];
+    }
+  };
+  // One memory round trip for the records and the first rows: the rows depend on
+  // the slot range alone, not on the merged frame.
   const float4 rec0 = record(0);
+  float4 v0[COMBINE_BATCH][2];
+  load_batch(v0, 0, 0, min(64, S));
   float mx = rec0.x;
   for (int s0 = 64; s0 < S; s0 += 64) mx = fmaxf(mx, record(s0).x);
   mx = wave_max(mx);  // the merged frame
@@ -617,13 +638,14 @@ __device__ __forceinline__ void combine_head(int t, int h, int H, int S, int bas
     const int n = min(64, S - s0);
     for (int j0 = 0; j0 < n; j0 += COMBINE_BATCH) {
       float4 v[COMBINE_BATCH][2];
+      if (s0 == 0 && j0 == 0) {
 #pragma unroll
-      for (int j = 0; j < COMBINE_BATCH; ++j) {
-        const int jj = min(j0 + j, n - 1);
-        const float4* src =
-            reinterpret_cast<const float4*>(ws_o + ((size_t)(base + s0 + jj) * H + h) * DV) + 2 * lane;
-        v[j][0] = src[0];
-        v[j][1] = src[1];
+        for (int j = 0; j < COMBINE_BATCH; ++j) {
+          v[j][0] = v0[j][0];
+          v[j][1] = v0[j][1];
+        }
+      } else {
+        load_batch(v, s0, j0, n);
       }
 #pragma unroll
       for (int j = 0; j < COMBINE_BATCH; ++j) {
@@ -660,15 +682,23 @@ __global__ __launch_bounds__(64 * COMBINE_WAVES) void combine_kernel(
     SasFwdArgs a, const int* __restrict__ plan, const float* __restrict__ ws_o,
     const float* __restrict__ ws_ml, uint16_t* __restrict__ out, float* __restrict__ lse) {
   const int H = a.H;
-  if (!plan_matches(plan, a)) return;  // refused plan: the attention kernel wrote zeros
-  const int items = plan[PH_NSPLIT_TOKENS] * H;  // (split token, head) pairs
   const SasPlanLayout L = sas_plan_layout(a.T, a.split_cap);
   const int wave = blockIdx.x * COMBINE_WAVES + (threadIdx.x >> 6);
+  // The split token's record (token, split count, first slot) is loaded with the
+  // plan header, before the header says how many split tokens there are: its
+  // index is clamped into the list, and a record past the count is never used.
+  auto split_record = [&](int i) {
+    const int ic = min(i, (int)L.split_cap - 1);
+    return make_int3(plan[L.off_split_tokens + ic], plan[L.off_split_meta + 2 * ic],
+                     plan[L.off_split_meta + 2 * ic + 1]);
+  };
+  int3 rec = split_record(wave / H);
+  if (!plan_matches(plan, a)) return;  // refused plan: the attention kernel wrote zeros
+  const int items = plan[PH_NSPLIT_TOKENS] * H;  // (split token, head) pairs
   for (int item = wave; item < items; item += gridDim.x * COMBINE_WAVES) {
     const int i = item / H, h = item - i * H;
-    const int t = plan[L.off_split_tokens + i];
-    const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
-    combine_head<QT>(t, h, H, tk[TK_SPLITS], tk[TK_WSBASE], ws_o, ws_ml, out, lse);
+    if (item != wave) rec = split_record(i);
+    combine_head<QT>(rec.x, h, H, rec.y, rec.z, ws_o, ws_ml, out, lse);
   }
 }
 

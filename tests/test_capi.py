@@ -109,19 +109,21 @@ def test_plan_header_mirror_matches_c_header():
     assert int(re.search(r"#define SAS_PLAN_MAGIC (0x[0-9A-Fa-f]+)", txt).group(1), 16) == M.PLAN_MAGIC
 
 
-@pytest.mark.parametrize("T,cores", [(1, 256), (256, 256), (8192, 256), (6, 1024)])
-def test_plan_and_workspace_sizes(T, cores):
-    """Plan: header, 8 ints per token, 4 per unit (capacity T + target), one per
-    possible split token (target).  Workspace: a 256-B status word region first,
-    then the row lists of every token (window + top-k slots), their addresses,
+@pytest.mark.parametrize("T,cores,topk", [(1, 256, 2048), (256, 256, 2048), (8192, 256, 2048),
+                                          (6, 1024, 2048), (5, 256, 2000)])
+def test_plan_and_workspace_sizes(T, cores, topk):
+    """Plan: header, 8 ints per token, 4 per unit (capacity T + target), 3 per
+    possible split token (target: its token, split count and first slot).
+    Workspace: a 256-B status word region first, then the row lists of every
+    token (window + top-k slots, spaced at whole 32-row tiles), their addresses,
     the counts, a copy of the plan and 2 * target partial slots."""
     from dsv4_planb_amd import metadata as M
 
     lib = _lib.load()
-    p = _good(total_tokens=T, num_cus=cores, topk=2048, num_heads_q=128)
+    p = _good(total_tokens=T, num_cus=cores, topk=topk, num_heads_q=128)
     n = ctypes.c_size_t()
     assert lib.sas_plan_size(ctypes.byref(p), ctypes.byref(n)) == 0
-    expect = M.PLAN_HDR + M.PLAN_TOK_W * T + M.PLAN_UNIT_W * (T + cores) + cores
+    expect = M.PLAN_HDR + M.PLAN_TOK_W * T + M.PLAN_UNIT_W * (T + cores) + 3 * cores
     assert n.value == (expect + 1 if expect == 1024 else expect)
     ws = ctypes.c_size_t()
     assert lib.sas_workspace_size(ctypes.byref(p), ctypes.byref(ws)) == 0
@@ -129,7 +131,7 @@ def test_plan_and_workspace_sizes(T, cores):
     def al(x):
         return (x + 255) // 256 * 256
 
-    stride = 128 + 2048
+    stride = (128 + topk + 31) // 32 * 32
     expect_ws = (al(4) + al(T * stride * 4) + al((T * stride + 32) * 8) + al(T * 4) + al(n.value * 4)
                  + al(2 * cores * 128 * 512 * 4) + al(2 * cores * 128 * 16))
     assert ws.value == expect_ws

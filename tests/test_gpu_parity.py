@@ -443,6 +443,12 @@ def test_device_plan_covers_every_row_once(cores):
                 assert tok[t, 7] == -1 and t not in stoks
     assert not by_tok, f"units for tokens no batch owns: {list(by_tok)[:5]}"
     assert (used == 1).all(), "split workspace slots overlap or go unused"
+    # after the split-token list (capacity: the balance target), each split token's
+    # split count and first slot, as its token record has them
+    split_cap = int(p[5])
+    smeta = p[M.PLAN_HDR + M.PLAN_TOK_W * T + M.PLAN_UNIT_W * unit_cap + split_cap:][:2 * nsplit_tok]
+    for i, t in enumerate(stoks.tolist()):
+        assert (smeta[2 * i], smeta[2 * i + 1]) == (tok[t, 6], tok[t, 7]), (i, t)
 
 
 def _plan_units(q_lens, kv, K, cores, with_plan=False):
