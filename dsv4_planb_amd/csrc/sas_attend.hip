@@ -160,6 +160,17 @@ __device__ __forceinline__ void vgpr_mfma_drain(f32x16_t& d) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(d));
 }
 
+// d = a b^T + 0 / d += a b^T on 32 x 32 x 64 e4m3 operands (8 VGPRs each): lane l
+// holds row / column l % 32 and k = 32 (l >> 5) .. + 31, one code per byte.  A
+// 16-pass XDL op: its result needs 20 wait states before a VALU read.
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ void vmfma8_first(f32x16_t& d, const i32x8_t& a, const i32x8_t& b) {
+  asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void vmfma8_acc(f32x16_t& d, const i32x8_t& a, const i32x8_t& b) {
+  asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+v"(d) : "v"(a), "v"(b));
+}
+
 #define SB() __builtin_amdgcn_sched_barrier(0)
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
@@ -244,12 +255,22 @@ __device__ __forceinline__ bool attend_unit(
   // fp8: K k-steps 2 j, 2 j + 1 come from one b128 read of row li, chunk 2 j + g at
   // position (2 j + g) ^ 9 b3 (b3 = (li >> 3) & 1): byte 32 (j ^ 4 b3) + 16 (g ^ b3),
   // i.e. kofs[(j >> 2) & 1] + 32 (j & ~4).
-  uint32_t kofs[2], kofs_r = 0;
+  // fp8 KV, bf16 queries (F8Q): QK runs on the fp8 MFMA, 64 dimensions per op.  Op m
+  // takes row li, dimensions 64 m + 32 g .. + 31: chunks c = 4 m + 2 g + {0, 1} at
+  // positions c ^ 9 b3, i.e. bytes k8o[j][h] + 64 (m & ~2) with h = (m >> 1) & 1.
+  constexpr bool F8Q = KV8 && QT == 0;
+  constexpr int QM = DQK / 64;  // fp8 ops per QK chain: 9 / 8
+  uint32_t kofs[2], kofs_r = 0, k8o[2][2];
   if constexpr (KV8) {
     const uint32_t b3 = (li >> 3) & 1;
     const uint32_t base = li * KV8_STRIDE + 16 * (g ^ b3);
     kofs[0] = base + 128 * b3;
     kofs[1] = base + 128 * (1 - b3);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      k8o[0][h] = li * KV8_STRIDE + 32 * g + 16 * b3 + 128 * (h ^ b3);
+      k8o[1][h] = k8o[0][h] + 16 - 32 * b3;
+    }
   } else {
     const int f = swz_a(li);
 #pragma unroll
@@ -325,13 +346,63 @@ __device__ __forceinline__ bool attend_unit(
     return false;
   }
 
-  u32x4_t qf[KSTEPS];
+  u32x4_t qf[F8Q ? 1 : KSTEPS];
+  // F8Q: the query, scaled by 2^e so that its largest |q| lies in [128, 256), as two
+  // e4m3 parts hi = rne(q 2^e) and lo = rne(q 2^e - hi), op m's B operands.  A bf16
+  // value has 8 significant bits and each part 4: hi + lo = q 2^e exactly for every
+  // element of magnitude >= 2^-10 of the head's largest (smaller ones are off by at
+  // most 2^-10 in the scaled units), so S 2^-e is the bf16 product.  ck = c 2^-e.
+  i32x8_t qh[F8Q ? QM : 1], ql[F8Q ? QM : 1];
+  float ck = a.scale_log2;
   {
     const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(q + ((size_t)t * H + hc) * DQK);
-    // fp8: k-step 2 j + h covers dimensions 32 j + 16 g + 8 h .. + 7 (the K order)
+    if constexpr (F8Q) {
+      u32x4_t raw[4 * QM];  // op m, lane half g: dimensions 64 m + 32 g + 8 j .. + 7
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-      qf[ks] = KV8 ? qrow[4 * (ks >> 1) + 2 * g + (ks & 1)] : qrow[2 * ks + g];
+      for (int m = 0; m < QM; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) raw[4 * m + j] = qrow[8 * m + 4 * g + j];
+      // the head's largest |q| over both half-waves (bf16 magnitudes order as integers)
+      uint32_t mx = 0;
+#pragma unroll
+      for (int i = 0; i < 4 * QM; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t w = raw[i][e] & 0x7fff7fffu;
+          mx = max(mx, max(w & 0xffffu, w >> 16));
+        }
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
+        mx = max(sw[0], sw[1]);
+      }
+      const float qmax = __uint_as_float(mx << 16);
+      const int e = qmax > 0.f ? min(max(8 - __builtin_amdgcn_frexp_expf(qmax), -100), 100) : 0;
+      const float qs = __builtin_amdgcn_ldexpf(1.f, e);
+      ck = a.scale_log2 * __builtin_amdgcn_ldexpf(1.f, -e);
+#pragma unroll
+      for (int m = 0; m < QM; ++m)
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {  // codes 4 d .. 4 d + 3 of op m
+          const uint32_t w0 = raw[4 * m + (d >> 1)][2 * (d & 1)];
+          const uint32_t w1 = raw[4 * m + (d >> 1)][2 * (d & 1) + 1];
+          const float a0 = __uint_as_float(w0 << 16) * qs, a1 = __uint_as_float(w0 & 0xffff0000u) * qs;
+          const float a2 = __uint_as_float(w1 << 16) * qs, a3 = __uint_as_float(w1 & 0xffff0000u) * qs;
+          int hw = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false);
+          hw = __builtin_amdgcn_cvt_pk_fp8_f32(a2, a3, hw, true);
+          const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hw, false);
+          const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hw, true);
+          int lw = __builtin_amdgcn_cvt_pk_fp8_f32(a0 - h01[0], a1 - h01[1], 0, false);
+          lw = __builtin_amdgcn_cvt_pk_fp8_f32(a2 - h23[0], a3 - h23[1], lw, true);
+          qh[m][d] = hw;
+          ql[m][d] = lw;
+        }
+    } else {
+      // fp8 (fp16 queries): k-step 2 j + h covers dimensions 32 j + 16 g + 8 h .. + 7
+      // (the K order)
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        qf[ks] = KV8 ? qrow[4 * (ks >> 1) + 2 * g + (ks & 1)] : qrow[2 * ks + g];
+    }
   }
   f32x16_t acc[16];
 #pragma unroll
@@ -432,8 +503,44 @@ __device__ __forceinline__ bool attend_unit(
   auto kpair8 = [&](const lds_u8* tl, int j) -> u32x4_t {
     return lds_read_b128(tl + kofs[(j >> 2) & 1] + 32 * (j & ~4));
   };
+  // F8Q: K operand of op m (two b128 reads of row li)
+  auto kread8 = [&](const lds_u8* tl, int m) -> i32x8_t {
+    const int h = (m >> 1) & 1, off = 64 * (m & ~2);
+    const u32x4_t c0 = lds_read_b128(tl + k8o[0][h] + off);
+    const u32x4_t c1 = lds_read_b128(tl + k8o[1][h] + off);
+    return i32x8_t{(int)c0[0], (int)c0[1], (int)c0[2], (int)c0[3],
+                   (int)c1[0], (int)c1[1], (int)c1[2], (int)c1[3]};
+  };
   auto qk = [&](const lds_u8* tl, f32x16_t& s, auto&& work) {
-    if constexpr (KV8) {
+    if constexpr (F8Q) {
+      // op m with hi, then with lo (the K operand read once); two work items per op,
+      // whose 64 cycles match two 16-bit k-steps, so the schedule's steps are kept
+      i32x8_t kr[2];
+      kr[0] = kread8(tl, 0);
+      SB();
+      work(-1);
+      SB();
+#pragma unroll
+      for (int m = 0; m < QM; ++m) {
+        if (m == 0)
+          vmfma8_first(s, kr[0], qh[0]);
+        else
+          vmfma8_acc(s, kr[m & 1], qh[m]);
+        if (m + 1 < QM) kr[(m + 1) & 1] = kread8(tl, m + 1);
+        work(4 * m);
+        SB();
+        work(4 * m + 1);
+        SB();
+        vmfma8_acc(s, kr[m & 1], ql[m]);
+        work(4 * m + 2);
+        SB();
+        work(4 * m + 3);
+        SB();
+      }
+      work(KSTEPS);
+      SB();
+      return;
+    } else if constexpr (KV8) {
       u32x4_t rw[2];
       rw[0] = kpair8(tl, 0);
       rw[1] = kpair8(tl, 1);
@@ -655,8 +762,8 @@ __device__ __forceinline__ bool attend_unit(
         x0 -= m_run;
         x1 -= m_run;
       } else if constexpr (KV8) {
-        x0 = fmaf(x0, c * sc[0], -m_run);
-        x1 = fmaf(x1, c * sc[1], -m_run);
+        x0 = fmaf(x0, ck * sc[0], -m_run);
+        x1 = fmaf(x1, ck * sc[1], -m_run);
       } else {
         x0 = fmaf(x0, c, -m_run);
         x1 = fmaf(x1, c, -m_run);
@@ -736,7 +843,7 @@ __device__ __forceinline__ bool attend_unit(
 #pragma unroll
       for (int r = 0; r < 8; r += 2) {
         const int rr = 8 * ks + r;
-        float x0 = x[rr] * (c * s16_at(s16, rr)), x1 = x[rr + 1] * (c * s16_at(s16, rr + 1));
+        float x0 = x[rr] * (ck * s16_at(s16, rr)), x1 = x[rr + 1] * (ck * s16_at(s16, rr + 1));
         asm volatile("" : "+v"(x0), "+v"(x1));
         x[rr] = x0;
         x[rr + 1] = x1;
@@ -787,7 +894,7 @@ __device__ __forceinline__ bool attend_unit(
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) s16[qd] = scl4(tc, qd);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] *= c * s16_at(s16, r);
+      for (int r = 0; r < 16; ++r) x[r] *= ck * s16_at(s16, r);
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] *= c;
@@ -835,6 +942,7 @@ __device__ __forceinline__ bool attend_unit(
     qk(tiles, s_cur, [](int) {});
     // S(0) is read by VALU next: wait out the XDL-write -> VALU-read hazard
     vgpr_mfma_drain(s_cur);
+    if constexpr (F8Q) asm volatile("s_nop 7" : "+v"(s_cur));
 
     // One PV call site for every tile: the O accumulators are inline-assembly
     // operands, and two call sites in the loop would be given different AGPRs,
