@@ -154,6 +154,7 @@ def make_case(
     dist: str = "normal",
     pool_pages: Optional[int] = None,
     cmp_pool_pages: Optional[int] = None,
+    q_spread: bool = False,
 ) -> Case:
     """``dist="normal"``: q and KV ~ N(0, value_scale^2) (the benchmark
     configurations).  ``dist="reference"``: the reference suite's own draws --
@@ -163,7 +164,11 @@ def make_case(
     ``pool_pages`` / ``cmp_pool_pages``: a shared page pool of that many pages,
     each sequence's block table a random permutation of it (truncated to the
     sequence's pages), so long contexts fit host memory; otherwise every
-    sequence owns its pages (one random permutation over all of them)."""
+    sequence owns its pages (one random permutation over all of them).
+
+    ``q_spread``: every head's queries scaled by its own 2^u, u in [-6, 2], and
+    every element by 2^v, v in [-12, 0]; head 0 all zeros.  Magnitudes then span
+    about 2^20 within a call and 2^12 within a head."""
     rng = np.random.default_rng(seed)
     seq_kv = [int(x) for x in seq_kv]
     qps = [int(q_per_seq)] * B if isinstance(q_per_seq, int) else [int(x) for x in q_per_seq]
@@ -178,6 +183,10 @@ def make_case(
         return x if value_scale == 1.0 else x * np.float32(value_scale)
 
     q = draw((T, H, D), (-10.0, 10.0))
+    if q_spread:
+        q = q * np.exp2(rng.uniform(-6.0, 2.0, size=(1, H, 1))).astype(np.float32)
+        q = q * np.exp2(rng.uniform(-12.0, 0.0, size=q.shape)).astype(np.float32)
+        q[:, 0, :] = 0.0
     q_bits = _encode(q, q_dtype)
 
     def paged_pool(lens: List[int], bs: int, lo_hi, shared: Optional[int]):

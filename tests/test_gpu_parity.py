@@ -113,6 +113,17 @@ def _fp8_edges():
                                                scenario=3, K=1024, q_dtype="fp16",
                                                kv_dtype="fp8e4m3", seed=31),
      {"core_num": 4}, "baseline"),
+    # bf16 queries with fp8 KV take QK on the fp8 MFMA, the query split into two e4m3
+    # parts under a per-head power-of-two scale: heads and elements of very different
+    # magnitudes (and an all-zero head), long units, both d_qk
+    ("fp8_q_spread_long_units", lambda: make_case(B=2, H=128, seq_kv=[9000, 3000], q_per_seq=2,
+                                                  scenario=3, K=1024, kv_dtype="fp8e4m3", seed=32,
+                                                  q_spread=True),
+     {"core_num": 4}, "baseline"),
+    ("fp8_d512_q_spread", lambda: make_case(B=2, H=64, D=512, seq_kv=[7000, 2000], q_per_seq=1,
+                                            scenario=3, K=512, kv_dtype="fp8e4m3", seed=33,
+                                            q_spread=True),
+     {"core_num": 4}, "baseline"),
 ])
 def test_fp8_paths(name, build, extra, rule):
     c = build()
