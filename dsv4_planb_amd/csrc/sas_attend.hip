@@ -354,21 +354,33 @@ __device__ __forceinline__ bool attend_unit(
   // most 2^-10 in the scaled units), so S 2^-e is the bf16 product.  ck = c 2^-e.
   i32x8_t qh[F8Q ? QM : 1], ql[F8Q ? QM : 1];
   float ck = a.scale_log2;
+  u32x4_t qraw[F8Q ? 4 * QM : 1];  // F8Q: op m, lane half g: dimensions 64 m + 32 g + 8 j .. + 7
   {
     const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(q + ((size_t)t * H + hc) * DQK);
     if constexpr (F8Q) {
-      u32x4_t raw[4 * QM];  // op m, lane half g: dimensions 64 m + 32 g + 8 j .. + 7
 #pragma unroll
       for (int m = 0; m < QM; ++m)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) raw[4 * m + j] = qrow[8 * m + 4 * g + j];
+        for (int j = 0; j < 4; ++j) qraw[4 * m + j] = qrow[8 * m + 4 * g + j];
+    } else {
+      // fp8 (fp16 queries): k-step 2 j + h covers dimensions 32 j + 16 g + 8 h .. + 7
+      // (the K order)
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        qf[ks] = KV8 ? qrow[4 * (ks >> 1) + 2 * g + (ks & 1)] : qrow[2 * ks + g];
+    }
+  }
+  // F8Q: the split, run once the first tiles' DMAs are issued (its VALU work then
+  // overlaps their flight instead of delaying it)
+  auto split_query = [&]() {
+    if constexpr (F8Q) {
       // the head's largest |q| over both half-waves (bf16 magnitudes order as integers)
       uint32_t mx = 0;
 #pragma unroll
       for (int i = 0; i < 4 * QM; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t w = raw[i][e] & 0x7fff7fffu;
+          const uint32_t w = qraw[i][e] & 0x7fff7fffu;
           mx = max(mx, max(w & 0xffffu, w >> 16));
         }
       {
@@ -383,8 +395,8 @@ __device__ __forceinline__ bool attend_unit(
       for (int m = 0; m < QM; ++m)
 #pragma unroll
         for (int d = 0; d < 8; ++d) {  // codes 4 d .. 4 d + 3 of op m
-          const uint32_t w0 = raw[4 * m + (d >> 1)][2 * (d & 1)];
-          const uint32_t w1 = raw[4 * m + (d >> 1)][2 * (d & 1) + 1];
+          const uint32_t w0 = qraw[4 * m + (d >> 1)][2 * (d & 1)];
+          const uint32_t w1 = qraw[4 * m + (d >> 1)][2 * (d & 1) + 1];
           const float a0 = __uint_as_float(w0 << 16) * qs, a1 = __uint_as_float(w0 & 0xffff0000u) * qs;
           const float a2 = __uint_as_float(w1 << 16) * qs, a3 = __uint_as_float(w1 & 0xffff0000u) * qs;
           int hw = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false);
@@ -396,14 +408,8 @@ __device__ __forceinline__ bool attend_unit(
           qh[m][d] = hw;
           ql[m][d] = lw;
         }
-    } else {
-      // fp8 (fp16 queries): k-step 2 j + h covers dimensions 32 j + 16 g + 8 h .. + 7
-      // (the K order)
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks)
-        qf[ks] = KV8 ? qrow[4 * (ks >> 1) + 2 * g + (ks & 1)] : qrow[2 * ks + g];
     }
-  }
+  };
   f32x16_t acc[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = f32x16_t{};
@@ -937,6 +943,7 @@ __device__ __forceinline__ bool attend_unit(
     ra_next = load_addrs(3);
 
     f32x16_t s_cur, s_next;
+    split_query();
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * CPT, 15));  // tile 0 landed
     wait_barrier();
     qk(tiles, s_cur, [](int) {});
@@ -1028,18 +1035,25 @@ __device__ __forceinline__ bool attend_unit(
   if (!hvalid) return false;
   if (splits == 1) {
     const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
-    if constexpr (KV8) {  // register 4 q + e of block mb: d = 32 mb + 8 q + 4 g + e
-      uint16_t* orow = out + ((size_t)t * H + h) * DV + 4 * g;
+    if constexpr (KV8) {
+      // Register 4 q + e of block mb holds d = 32 mb + 8 q + 4 g + e.  For q = 2 p and
+      // 2 p + 1, packed as a and b, one permlane32 swap of (a, b) leaves half-wave 0
+      // with (its a, half 1's a) = d 16 p .. + 7 and half-wave 1 with (half 0's b, its
+      // b) = d 16 p + 8 .. + 15: 16-B stores, as for 16-bit KV.
+      uint16_t* orow = out + ((size_t)t * H + h) * DV + 8 * g;
 #pragma unroll
       for (int mb = 0; mb < 16; ++mb) {
         f32x16_t v = acc[mb];
         asm volatile("" : "+v"(v));
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          uint2 o;
-          o.x = pack2_q16<QT>(v[4 * qd] * inv, v[4 * qd + 1] * inv);
-          o.y = pack2_q16<QT>(v[4 * qd + 2] * inv, v[4 * qd + 3] * inv);
-          *reinterpret_cast<uint2*>(orow + 32 * mb + 8 * qd) = o;
+        for (int p = 0; p < 2; ++p) {
+          const uint32_t a0 = pack2_q16<QT>(v[8 * p] * inv, v[8 * p + 1] * inv);
+          const uint32_t a1 = pack2_q16<QT>(v[8 * p + 2] * inv, v[8 * p + 3] * inv);
+          const uint32_t b0 = pack2_q16<QT>(v[8 * p + 4] * inv, v[8 * p + 5] * inv);
+          const uint32_t b1 = pack2_q16<QT>(v[8 * p + 6] * inv, v[8 * p + 7] * inv);
+          const auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+          *reinterpret_cast<u32x4_t*>(orow + 32 * mb + 16 * p) = u32x4_t{s0[0], s1[0], s0[1], s1[1]};
         }
       }
       if (lse && g == 0) lse[(size_t)t * H + h] = (m_run + __log2f(l_e)) * 0.6931471805599453f;
