@@ -388,7 +388,11 @@ __device__ __forceinline__ bool attend_unit(
         mx = max(sw[0], sw[1]);
       }
       const float qmax = __uint_as_float(mx << 16);
-      const int e = qmax > 0.f ? min(max(8 - __builtin_amdgcn_frexp_expf(qmax), -100), 100) : 0;
+      // |e| <= 126 keeps 2^e and 2^-e normal floats: every finite bf16 qmax up to
+      // 2^128 is placed in [128, 256); only a head whose largest |q| is below 2^-118
+      // is placed lower (off by at most 2^-136 per element, far below its own size
+      // times 2^-8 that bf16 rounding already allows)
+      const int e = qmax > 0.f ? min(max(8 - __builtin_amdgcn_frexp_expf(qmax), -126), 126) : 0;
       const float qs = __builtin_amdgcn_ldexpf(1.f, e);
       ck = a.scale_log2 * __builtin_amdgcn_ldexpf(1.f, -e);
 #pragma unroll
