@@ -109,6 +109,12 @@ __device__ __forceinline__ int swz_b(int r) { return (r >> 1) & 7; }
 constexpr int KV8_STRIDE = 1056;
 constexpr int KV8_SCALES = SAS_TILE * KV8_STRIDE;
 
+// Epilogue staging: each wave's 32 output rows (1 KB each: 512 16-bit values, or half a
+// row of fp32 partials) at a 1040-B stride, which spreads the rows' 16-B writes over
+// the banks.
+constexpr int EPI_STRIDE = 1040;
+constexpr int EPI_WAVE = 32 * EPI_STRIDE;
+
 template <int DQK, bool KV8>
 struct AttendLds {
   static constexpr int TILEB =
@@ -196,7 +202,7 @@ constexpr int gather_cpol() { return STREAM ? 2 : 0; }  // 2: the NT bit of the 
 template <int DQK, int QT, bool STREAM, bool KV8, bool REDO>
 __device__ __forceinline__ bool attend_unit(
     int u, AttendLds<DQK, KV8>& sm, const SasFwdArgs& a, const uint16_t* __restrict__ q,
-    const uint64_t* addr_list, const float* scale_list, int ncmp_t,
+    const uint64_t* addr_list, const float* scale_list, const int* ncmp, int ncmp_t,
     const float* __restrict__ sinks, const int* __restrict__ plan, uint16_t* __restrict__ out,
     float* __restrict__ lse, float* __restrict__ ws_o, float* __restrict__ ws_ml, float& m_obs) {
   constexpr int DV = 512;
@@ -215,7 +221,11 @@ __device__ __forceinline__ bool attend_unit(
   // rows and their scales and inverse scales
   constexpr int CPT = KV8 ? 10 : 8 + (ROPE ? 8 : 0);
   static_assert(TILE == 32, "the MFMA tiling assumes 32-key tiles");
+  // fp8 KV with bf16 queries: QK on the fp8 MFMA, 64 dimensions per op
+  constexpr bool F8Q = KV8 && QT == 0;
+  constexpr int QM = DQK / 64;  // fp8 ops per QK chain: 9 / 8
   static_assert(AttendLds<DQK, KV8>::TILEB == TILEB, "LDS layout");
+  static_assert(4 * EPI_WAVE <= 4 * TILEB, "the epilogue staging fits the ring");
   lds_u8* const tiles = (lds_u8*)sm.tiles;
 
   const int tid = threadIdx.x;
@@ -236,11 +246,57 @@ __device__ __forceinline__ bool attend_unit(
     return false;
   }
 
+  const int r0 = ur[1];
+  // Head indices past H are clamped onto a valid head and never stored.
+  const int h = w * 32 + li;
+  const bool hvalid = h < H;
+  const int hc = min(h, H - 1);
+  // the head's sink, read by every unit (first, so that the wait for it is not a wait
+  // for the loads below: vector loads complete in order)
+  const float sink_raw = sinks[hc];
+
+  // The first three tiles' row addresses of this wave (lane 8 i + k: tile i, row
+  // 8 w + k) in one vector load, issued with the query's loads before the token record
+  // is read: one memory round trip for the unit's start, where a scalar load per tile
+  // chains three.  Rows past the unit's end become the zero row once the end is known.
+  // The load itself stays inside the unit's own planned rows [r0, ur[2]) (clamped), so
+  // it never touches lines another unit writes when the units resolve their own rows.
+  // (Lanes 24 .. 63 load tile 3's rows and repeats, unused: no divergent branch, which
+  // would move the list pointer to VGPRs.)
+  const int pro_row = r0 + ((lane >> 3) & 3) * TILE + 8 * w + (lane & 7);
+  const int pro_ld = min(max(min(pro_row, ur[2] - 1), r0), a.list_stride - 1);
+  // (a global load: through a generic pointer it would be a FLAT load, which every
+  // later wait on vector or LDS counters has to drain)
+  typedef __attribute__((address_space(1))) const uint64_t g_u64;
+  uint64_t pro_addr = ((g_u64*)(uintptr_t)addr_list)[(size_t)t * a.list_stride + pro_ld];
+  // The fence keeps this load ahead of the query's (vector loads complete in order:
+  // the DMAs then wait for the addresses only, not for the query too).
+  asm volatile("" ::: "memory");
+  u32x4_t qf[F8Q ? 1 : KSTEPS];
+  u32x4_t qraw[F8Q ? 4 * QM : 1];  // F8Q: op m, lane half g: dimensions 64 m + 32 g + 8 j .. + 7
+  {
+    const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(q + ((size_t)t * H + hc) * DQK);
+    if constexpr (F8Q) {
+#pragma unroll
+      for (int m = 0; m < QM; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qraw[4 * m + j] = qrow[8 * m + 4 * g + j];
+    } else {
+      // fp8 (fp16 queries): k-step 2 j + h covers dimensions 32 j + 16 g + 8 h .. + 7
+      // (the K order)
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        qf[ks] = KV8 ? qrow[4 * (ks >> 1) + 2 * g + (ks & 1)] : qrow[2 * ks + g];
+    }
+  }
+
   const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
   const int nwin = min(tk[TK_NWIN], a.win_left + 1);
   const int splits = tk[TK_SPLITS], wsbase = tk[TK_WSBASE];
-  const int r0 = ur[1];
-  const int r1 = min(min(ur[2], nwin + ncmp_t), a.list_stride);
+  // the token's compressed row count: read here, with the token record (one round
+  // trip for both), unless the unit resolved its rows itself (ncmp_t >= 0)
+  const int nc = ncmp_t >= 0 ? ncmp_t : ncmp[t];
+  const int r1 = min(min(ur[2], nwin + nc), a.list_stride);
   const int ntiles = r1 > r0 ? (r1 - r0 + TILE - 1) / TILE : 0;
   // row addresses of this unit's list (pool addresses; -1 codes read the zero row)
   const uint64_t* alist = addr_list + (size_t)t * a.list_stride + r0;
@@ -258,8 +314,6 @@ __device__ __forceinline__ bool attend_unit(
   // fp8 KV, bf16 queries (F8Q): QK runs on the fp8 MFMA, 64 dimensions per op.  Op m
   // takes row li, dimensions 64 m + 32 g .. + 31: chunks c = 4 m + 2 g + {0, 1} at
   // positions c ^ 9 b3, i.e. bytes k8o[j][h] + 64 (m & ~2) with h = (m >> 1) & 1.
-  constexpr bool F8Q = KV8 && QT == 0;
-  constexpr int QM = DQK / 64;  // fp8 ops per QK chain: 9 / 8
   uint32_t kofs[2], kofs_r = 0, k8o[2][2];
   if constexpr (KV8) {
     const uint32_t b3 = (li >> 3) & 1;
@@ -310,12 +364,8 @@ __device__ __forceinline__ bool attend_unit(
   }
 
   // ---- per-wave state: 32 heads per wave ----
-  // Head indices past H are clamped onto a valid head and never stored.
-  const int h = w * 32 + li;
-  const bool hvalid = h < H;
-  const int hc = min(h, H - 1);
   // golden.py:162-163: the unit holding the token's first rows carries the sink
-  const float sink2 = split == 0 ? sinks[hc] * LOG2E : -INFINITY;
+  const float sink2 = split == 0 ? sink_raw * LOG2E : -INFINITY;
 
   // A unit without rows (a redo always has some): O = 0 and the normalisers are
   // the sink's alone.  Returning here also keeps the accumulators below on a
@@ -346,7 +396,6 @@ __device__ __forceinline__ bool attend_unit(
     return false;
   }
 
-  u32x4_t qf[F8Q ? 1 : KSTEPS];
   // F8Q: the query, scaled by 2^e so that its largest |q| lies in [128, 256), as two
   // e4m3 parts hi = rne(q 2^e) and lo = rne(q 2^e - hi), op m's B operands.  A bf16
   // value has 8 significant bits and each part 4: hi + lo = q 2^e exactly for every
@@ -354,22 +403,6 @@ __device__ __forceinline__ bool attend_unit(
   // most 2^-10 in the scaled units), so S 2^-e is the bf16 product.  ck = c 2^-e.
   i32x8_t qh[F8Q ? QM : 1], ql[F8Q ? QM : 1];
   float ck = a.scale_log2;
-  u32x4_t qraw[F8Q ? 4 * QM : 1];  // F8Q: op m, lane half g: dimensions 64 m + 32 g + 8 j .. + 7
-  {
-    const u32x4_t* qrow = reinterpret_cast<const u32x4_t*>(q + ((size_t)t * H + hc) * DQK);
-    if constexpr (F8Q) {
-#pragma unroll
-      for (int m = 0; m < QM; ++m)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) qraw[4 * m + j] = qrow[8 * m + 4 * g + j];
-    } else {
-      // fp8 (fp16 queries): k-step 2 j + h covers dimensions 32 j + 16 g + 8 h .. + 7
-      // (the K order)
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks)
-        qf[ks] = KV8 ? qrow[4 * (ks >> 1) + 2 * g + (ks & 1)] : qrow[2 * ks + g];
-    }
-  }
   // F8Q: the split, run once the first tiles' DMAs are issued (its VALU work then
   // overlaps their flight instead of delaying it)
   auto split_query = [&]() {
@@ -423,7 +456,8 @@ __device__ __forceinline__ bool attend_unit(
   // Wave w copies rows 8 w .. 8 w + 7 of every tile.  Latent: instruction k copies
   // row 8 w + k, lane l fetching source chunk l ^ swz_a(8 w + k) =
   // l ^ ((2 w + (k >> 2)) & 3) into slot l.  Row addresses reach SGPRs by scalar
-  // loads an iteration before their DMA.
+  // loads an iteration before their DMA (tiles 0 .. 2: by lane reads of the
+  // prologue's vector load).
   const int wu = __builtin_amdgcn_readfirstlane(w);  // the wave index as a scalar
   const uint32_t ulane = (uint32_t)lane;
   // fp8: every row of wave w has bit 3 of its tile row equal to w & 1, so lane l
@@ -449,6 +483,19 @@ __device__ __forceinline__ bool attend_unit(
     // made before (its DMA waits count vector-memory instructions)
     typedef __attribute__((address_space(4))) const RowAddrs c_RowAddrs;
     return fix_tail(*(c_RowAddrs*)(uintptr_t)(alist + il * TILE + 8 * wu), i);
+  };
+  // Tile i < 3's row addresses, read out of the lanes of the prologue's vector load
+  // (rows past r1, dead tiles' included, already hold the zero row).  Tile 3's come
+  // by a scalar load: they stay live into the loop, where SGPRs filled from lanes
+  // push the fp8 variants' registers over the limit.
+  if (pro_row >= r1) pro_addr = (uint64_t)g_zero_row;
+  auto pro_addrs = [&](int i) -> RowAddrs {
+    RowAddrs ra;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      ra[k] = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(pro_addr >> 32), 8 * i + k) << 32) |
+              (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)pro_addr, 8 * i + k);
+    return ra;
   };
   // One row through a raw buffer resource based at the row (loads directly into
   // LDS, never the FLAT form: an outstanding FLAT load that writes LDS makes every
@@ -936,7 +983,7 @@ __device__ __forceinline__ bool attend_unit(
     RowAddrs ra_next;
 #pragma unroll
     for (int i0 = 0; i0 < 3; ++i0) {
-      ra_next = load_addrs(i0);
+      ra_next = pro_addrs(i0);
 #pragma unroll
       for (int k = 0; k < 8; ++k) dma_lat(i0, ra_next, k);
       if constexpr (KV8)
@@ -1035,71 +1082,83 @@ __device__ __forceinline__ bool attend_unit(
     }
   }
 
-  // ---- epilogue: lane (li, g) holds d = 32 mb + 16 g + r of head li ----
-  if (!hvalid) return false;
+  // ---- epilogue: the output leaves through LDS ----
+  // Each wave writes its 32 heads' rows into its own region of the ring (idle now:
+  // every wave has passed its last PV and its DMAs have landed, which the guard's
+  // barrier, or the redo's own below, establishes), then stores them one row per
+  // instruction: 64 lanes x 16 B, one contiguous 1 KB.  Stored straight from the
+  // accumulator layout, each instruction would write 32 B into each of 32 rows, which
+  // the memory pipeline moves at about a quarter of its rate.
+  // Accumulator layout: 16-bit KV: register r of block mb of lane (li, g) is d =
+  // 32 mb + 16 g + r of head li; fp8: register 4 q + e is d = 32 mb + 8 q + 4 g + e.
+  if constexpr (REDO) lds_barrier();
+  lds_u8* const ob = tiles + w * EPI_WAVE;
+  const int nrows = min(32, H - 32 * w);  // this wave's heads below H (wave-uniform)
+  // rows [0, nrows) of the wave's region to dst + r * row_elems (1 KB per row)
+  auto rows_out = [&](auto* dst, size_t row_elems) {
+#pragma unroll
+    for (int r0 = 0; r0 < 32; r0 += 8) {
+      u32x4_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = lds_read_b128(ob + (r0 + j) * EPI_STRIDE + 16 * lane);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (r0 + j < nrows)
+          *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint8_t*>(dst + (r0 + j) * row_elems) + 16 * lane) = v[j];
+    }
+  };
+  auto lds_w128 = [&](int off, u32x4_t v) {
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(ob + off) = v;
+  };
   if (splits == 1) {
     const float inv = l_w > 0.f ? 1.f / l_w : 0.f;
-    if constexpr (KV8) {
-      // Register 4 q + e of block mb holds d = 32 mb + 8 q + 4 g + e.  For q = 2 p and
-      // 2 p + 1, packed as a and b, one permlane32 swap of (a, b) leaves half-wave 0
-      // with (its a, half 1's a) = d 16 p .. + 7 and half-wave 1 with (half 0's b, its
-      // b) = d 16 p + 8 .. + 15: 16-B stores, as for 16-bit KV.
-      uint16_t* orow = out + ((size_t)t * H + h) * DV + 8 * g;
-#pragma unroll
-      for (int mb = 0; mb < 16; ++mb) {
-        f32x16_t v = acc[mb];
-        asm volatile("" : "+v"(v));
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const uint32_t a0 = pack2_q16<QT>(v[8 * p] * inv, v[8 * p + 1] * inv);
-          const uint32_t a1 = pack2_q16<QT>(v[8 * p + 2] * inv, v[8 * p + 3] * inv);
-          const uint32_t b0 = pack2_q16<QT>(v[8 * p + 4] * inv, v[8 * p + 5] * inv);
-          const uint32_t b1 = pack2_q16<QT>(v[8 * p + 6] * inv, v[8 * p + 7] * inv);
-          const auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
-          const auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
-          *reinterpret_cast<u32x4_t*>(orow + 32 * mb + 16 * p) = u32x4_t{s0[0], s1[0], s0[1], s1[1]};
-        }
-      }
-      if (lse && g == 0) lse[(size_t)t * H + h] = (m_run + __log2f(l_e)) * 0.6931471805599453f;
-      return false;
-    }
-    uint16_t* orow = out + ((size_t)t * H + h) * DV + 16 * g;
-    // One 16-register block at a time into VGPRs (the pin keeps the copies in
-    // step with the stores: copied all at once, the 256 accumulators overflow
-    // the VGPRs and spill).
+    // row li: bf16 / fp16 d = 0 .. 511 at 2 d
 #pragma unroll
     for (int mb = 0; mb < 16; ++mb) {
       f32x16_t v = acc[mb];
       asm volatile("" : "+v"(v));
+      if constexpr (KV8) {
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        u32x4_t o;
+        for (int q2 = 0; q2 < 4; ++q2) {
+          const uint32_t p0 = pack2_q16<QT>(v[4 * q2] * inv, v[4 * q2 + 1] * inv);
+          const uint32_t p1 = pack2_q16<QT>(v[4 * q2 + 2] * inv, v[4 * q2 + 3] * inv);
+          typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(
+              ob + li * EPI_STRIDE + 64 * mb + 16 * q2 + 8 * g) = u32x2_t{p0, p1};
+        }
+      } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          o[e] = pack2_q16<QT>(v[8 * hf + 2 * e] * inv, v[8 * hf + 2 * e + 1] * inv);
-        *reinterpret_cast<u32x4_t*>(orow + 32 * mb + 8 * hf) = o;
+        for (int hf = 0; hf < 2; ++hf) {
+          u32x4_t o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o[e] = pack2_q16<QT>(v[8 * hf + 2 * e] * inv, v[8 * hf + 2 * e + 1] * inv);
+          lds_w128(li * EPI_STRIDE + 64 * mb + 32 * g + 16 * hf, o);
+        }
       }
     }
-    if (lse && g == 0) lse[(size_t)t * H + h] = (m_run + __log2f(l_e)) * 0.6931471805599453f;
+    rows_out(out + ((size_t)t * H + 32 * w) * DV, DV);
+    if (lse && g == 0 && hvalid) lse[(size_t)t * H + h] = (m_run + __log2f(l_e)) * 0.6931471805599453f;
   } else {  // an un-normalised partial (O, m, l_w, l_e) for the combine pass
     const int slot = wsbase + split;
     if (slot < 0 || slot >= a.slot_cap) return false;  // (a sound plan never gets here)
-    // registers 4 qd .. 4 qd + 3 of block mb: d = 32 mb + 16 g + 4 qd .. (16-bit KV),
-    // 32 mb + 8 qd + 4 g .. (fp8)
-    float* orow = ws_o + ((size_t)slot * H + h) * DV + (KV8 ? 4 : 16) * g;
+    // fp32 rows, in two halves of 256 dimensions (1 KB per row each)
 #pragma unroll
-    for (int mb = 0; mb < 16; ++mb) {
+    for (int half = 0; half < 2; ++half) {
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        float4 v;
-        v.x = acc[mb][4 * qd + 0];
-        v.y = acc[mb][4 * qd + 1];
-        v.z = acc[mb][4 * qd + 2];
-        v.w = acc[mb][4 * qd + 3];
-        *reinterpret_cast<float4*>(orow + 32 * mb + (KV8 ? 8 : 4) * qd) = v;
+      for (int mb = 8 * half; mb < 8 * half + 8; ++mb) {
+        const int mo = 128 * (mb - 8 * half);
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          u32x4_t o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = __float_as_uint(acc[mb][4 * qd + e]);
+          lds_w128(li * EPI_STRIDE + mo + (KV8 ? 32 * qd + 16 * g : 64 * g + 16 * qd), o);
+        }
       }
+      rows_out(ws_o + ((size_t)slot * H + 32 * w) * DV + 256 * half, DV);
     }
-    if (g == 0)
+    if (g == 0 && hvalid)
       reinterpret_cast<float4*>(ws_ml)[(size_t)slot * H + h] = make_float4(m_run, l_w, l_e, 0.f);
   }
   return false;
@@ -1121,6 +1180,7 @@ __global__ __launch_bounds__(256, 1) void attend_kernel(
   __shared__ __attribute__((aligned(16))) AttendLds<DQK, KV8> sm;
   static_assert(sizeof(RsShared) <= sizeof(sm.tiles), "the resolution borrows the tile ring");
   const int u = blockIdx.x;
+  const int units = plan[PH_UNITS];  // (read with the header: one round trip)
   const bool plan_ok = plan_matches(plan, a);
   if (rs.addr && u == 0 && threadIdx.x == 0) *rs.status = plan_ok ? SAS_OK : SAS_ERR_PLAN;
   if (!plan_ok) {  // a plan built for other arguments: zeros (the call's status word
@@ -1132,10 +1192,11 @@ __global__ __launch_bounds__(256, 1) void attend_kernel(
     }
     return;
   }
-  if (u >= plan[PH_UNITS]) return;
+  if (u >= units) return;
   const int* ur = plan + SAS_PLAN_HDR + (size_t)SAS_TOK_W * a.T + (size_t)u * SAS_UNIT_W;
   const int t = ur[0];
-  int ncmp_t;  // the token's compressed row count (at least what this unit needs)
+  int ncmp_t = -1;  // resolved here: the token's compressed row count (at least what
+                    // this unit needs); -1: the unit reads it from ncmp
   if (rs.addr) {
     const int* tk = plan + SAS_PLAN_HDR + (size_t)t * SAS_TOK_W;
     const int split = ur[3];
@@ -1145,20 +1206,19 @@ __global__ __launch_bounds__(256, 1) void attend_kernel(
     // The token's last unit scans its list to the end: its count is exact.
     if (rs.ncmp && threadIdx.x == 0 && (split < 0 || split == tk[TK_SPLITS] - 1)) rs.ncmp[t] = ncmp_t;
     // Every wave's stores have reached L2 before any wave reads the lists back
-    // (scalar loads and the scale DMA), and every wave is done with the borrowed LDS.
+    // (vector and scalar loads, the scale DMA), and every wave is done with the
+    // borrowed LDS.
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  } else {
-    ncmp_t = ncmp[t];
   }
   // The lists are read through pointers the compiler cannot trace to the stores
   // above, so none of those loads moves before the barrier.
   asm volatile("" : "+s"(addr_list), "+s"(scale_list));
   float m_obs = 0.f;
-  if (attend_unit<DQK, QT, STREAM, KV8, false>(u, sm, a, q, addr_list, scale_list, ncmp_t, sinks, plan,
+  if (attend_unit<DQK, QT, STREAM, KV8, false>(u, sm, a, q, addr_list, scale_list, ncmp, ncmp_t, sinks, plan,
                                                out, lse, ws_o, ws_ml, m_obs)) {
     lds_barrier();  // every wave is done with the ring before the redo refills it
-    attend_unit<DQK, QT, STREAM, KV8, true>(u, sm, a, q, addr_list, scale_list, ncmp_t, sinks, plan,
-                                            out, lse, ws_o, ws_ml, m_obs);
+    attend_unit<DQK, QT, STREAM, KV8, true>(u, sm, a, q, addr_list, scale_list, ncmp, ncmp_t, sinks,
+                                            plan, out, lse, ws_o, ws_ml, m_obs);
   }
 }
 
