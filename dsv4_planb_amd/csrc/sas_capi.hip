@@ -289,6 +289,7 @@ int sas_plan(const sas_params_t* p, const int32_t* q_prefix, const int32_t* act_
   int rc = sas_validate(p);
   if (rc) return rc;
   if (!q_prefix || !act_q_lens || !seqused_kv || !plan) return SAS_ERR_NULL;
+  if (!aligned16(plan)) return SAS_ERR_SHAPE;  // the planner writes 16-B records
   const int target = target_units(p);
   if (plan_n < (size_t)sas_plan_layout(p->total_tokens, target).total) return SAS_ERR_PLAN;
   hipLaunchKernelGGL(sas::plan_kernel, dim3(1), dim3(sas::PLAN_NT), 0, (hipStream_t)stream,

@@ -43,9 +43,8 @@ struct TokInfo {
 // Token -> (batch, local position) through q_prefix / act_q: the owning batch is
 // the last b with q_prefix[b] <= t (equal prefixes only occur for empty batches,
 // which precede the batch that owns the tokens).
-__device__ TokInfo token_info(const SasPlanArgs& a, const int* __restrict__ q_prefix,
-                              const int* __restrict__ act_q, const int* __restrict__ seqused_kv,
-                              int t) {
+__device__ TokInfo token_info(const SasPlanArgs& a, const int* q_prefix, const int* act_q,
+                              const int* seqused_kv, int t) {
   TokInfo ti{-1, 0, 0, 0, 0, 0};
   int lo = 0, hi = a.B - 1, b = -1;
   while (lo <= hi) {
@@ -80,6 +79,13 @@ __device__ TokInfo token_info(const SasPlanArgs& a, const int* __restrict__ q_pr
 }
 
 constexpr int PLAN_NT = 1024;
+constexpr int PLAN_WAVES = PLAN_NT / 64;
+// Batches up to this many sequences have q_prefix / act_q / seqused_kv staged in LDS
+// for the token lookups (larger ones search global memory).
+constexpr int PLAN_LDS_B = 2048;
+// Up to this many tokens, each token's row count stays in LDS between the planner's
+// passes (beyond it, every pass recomputes it from the inputs).
+constexpr int PLAN_LDS_T = 8192;
 
 // Workgroup of the unit emitted k-th: within each full group of 16, emission order
 // 2j and 2j + 1 go to workgroups j and j + 8 (one XCD); the last partial group keeps
@@ -108,47 +114,78 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
                                                        const int* __restrict__ act_q,
                                                        const int* __restrict__ seqused_kv,
                                                        int* __restrict__ plan) {
-  __shared__ long long red[PLAN_NT];
-  __shared__ int scan_u[PLAN_NT], scan_s[PLAN_NT], scan_k[PLAN_NT];
-  const int tid = threadIdx.x;
+  // Every pass reads its inputs from LDS or registers: nothing the kernel stores is
+  // read back from global memory, and the reductions and the scan go through wave
+  // shuffles with one LDS step (two barriers each).
+  __shared__ int s_qp[PLAN_LDS_B], s_aq[PLAN_LDS_B], s_su[PLAN_LDS_B];
+  __shared__ int s_rows[PLAN_LDS_T];  // a token's rows, -1: no sequence owns it
+  __shared__ long long s_red[PLAN_WAVES];
+  __shared__ int s_wsum[3][PLAN_WAVES];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const SasPlanLayout L = sas_plan_layout(a.T, a.target);
   int* tok = plan + L.off_tok;
   int* units = plan + L.off_units;
   int* stoks = plan + L.off_split_tokens;
   int* smeta = plan + L.off_split_meta;
-  const int per = (a.T + PLAN_NT - 1) / PLAN_NT;
-  const int t0 = min(a.T, tid * per), t1 = min(a.T, t0 + per);
+  const bool staged_b = a.B <= PLAN_LDS_B, staged_t = a.T <= PLAN_LDS_T;
+  if (staged_b) {
+    for (int i = tid; i < a.B; i += PLAN_NT) {
+      s_qp[i] = q_prefix[i];
+      s_aq[i] = act_q[i];
+      s_su[i] = seqused_kv[i];
+    }
+    __syncthreads();
+  }
+  const int* qp = staged_b ? s_qp : q_prefix;
+  const int* aqp = staged_b ? s_aq : act_q;
+  const int* sup = staged_b ? s_su : seqused_kv;
 
+  // Token records (their first six fields) and row counts; tokens interleaved over
+  // the threads, so that the record stores are contiguous.
   long long my_rows = 0, my_longest = 0;
-  for (int t = t0; t < t1; ++t) {
-    TokInfo ti = token_info(a, q_prefix, act_q, seqused_kv, t);
+  for (int t = tid; t < a.T; t += PLAN_NT) {
+    const TokInfo ti = token_info(a, qp, aqp, sup, t);
     int* r = tok + (size_t)t * SAS_TOK_W;
-    r[TK_B] = ti.b;
-    r[TK_S] = ti.s;
-    r[TK_SG] = ti.sg;
-    r[TK_NWIN] = ti.nwin;
-    r[TK_WINLO] = ti.winlo;
-    r[TK_NCMPMAX] = ti.ncmpmax;
-    if (ti.b >= 0) {
-      my_rows += ti.nwin + ti.ncmpmax;
-      my_longest = max(my_longest, (long long)ti.nwin + ti.ncmpmax);
+    *reinterpret_cast<int4*>(r) = make_int4(ti.b, ti.s, ti.sg, ti.nwin);
+    *reinterpret_cast<int2*>(r + TK_WINLO) = make_int2(ti.winlo, ti.ncmpmax);
+    const int rows = ti.b >= 0 ? ti.nwin + ti.ncmpmax : -1;
+    if (staged_t) s_rows[t] = rows;
+    if (rows >= 0) {
+      my_rows += rows;
+      my_longest = max(my_longest, (long long)rows);
     }
   }
+  __syncthreads();
+  // token t's rows (-1: no sequence owns it)
+  auto tok_rows = [&](int t) -> int {
+    if (staged_t) return s_rows[t];
+    const TokInfo ti = token_info(a, qp, aqp, sup, t);
+    return ti.b >= 0 ? ti.nwin + ti.ncmpmax : -1;
+  };
   // Block-wide sum (max_op: maximum); every thread gets the result.
   auto block_reduce = [&](long long v, bool max_op) -> long long {
-    __syncthreads();  // earlier readers of red[0] are done
-    red[tid] = v;
-    __syncthreads();
-    for (int off = PLAN_NT / 2; off > 0; off >>= 1) {
-      if (tid < off) red[tid] = max_op ? max(red[tid], red[tid + off]) : red[tid] + red[tid + off];
-      __syncthreads();
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const long long o = __shfl_xor(v, off);
+      v = max_op ? max(v, o) : v + o;
     }
-    return red[0];
+    __syncthreads();  // earlier readers of s_red are done
+    if (lane == 0) s_red[wave] = v;
+    __syncthreads();
+    long long r = s_red[0];
+#pragma unroll
+    for (int i = 1; i < PLAN_WAVES; ++i) r = max_op ? max(r, s_red[i]) : r + s_red[i];
+    return r;
   };
   const long long R = block_reduce(my_rows, false);
   long long chunk = (R + a.target - 1) / a.target;
   if (chunk < SAS_MIN_CHUNK) chunk = SAS_MIN_CHUNK;
   chunk = (chunk + SAS_TILE - 1) / SAS_TILE * SAS_TILE;
+
+  // From here on each thread owns a contiguous range of tokens (the scan below gives
+  // its first unit, slot and split-token index).
+  const int per = (a.T + PLAN_NT - 1) / PLAN_NT;
+  const int t0 = min(a.T, tid * per), t1 = min(a.T, t0 + per);
   // Fewer tokens than target units: the smallest chunk (a multiple of the tile) whose
   // units number at most `target`, so that every unit starts in the first wave of
   // workgroups.  R / target alone leaves a second, partial wave of units after the
@@ -158,8 +195,7 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     auto units_at = [&](long long c) {
       long long n = 0;
       for (int t = t0; t < t1; ++t) {
-        const int* r = tok + (size_t)t * SAS_TOK_W;
-        const long long rows = r[TK_B] >= 0 ? (long long)r[TK_NWIN] + r[TK_NCMPMAX] : 0;
+        const long long rows = max(tok_rows(t), 0);
         n += rows > c ? (rows + c - 1) / c : 1;
       }
       return n;
@@ -179,8 +215,7 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
 
   int my_u = 0, my_s = 0, my_k = 0;
   for (int t = t0; t < t1; ++t) {
-    const int* r = tok + (size_t)t * SAS_TOK_W;
-    long long rows = r[TK_B] >= 0 ? (long long)r[TK_NWIN] + r[TK_NCMPMAX] : 0;
+    const long long rows = max(tok_rows(t), 0);
     int splits = rows > chunk ? (int)((rows + chunk - 1) / chunk) : 1;
     my_u += splits;
     if (splits > 1) {
@@ -188,35 +223,46 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
       my_k += 1;
     }
   }
-  scan_u[tid] = my_u;
-  scan_s[tid] = my_s;
-  scan_k[tid] = my_k;
-  __syncthreads();
-  for (int off = 1; off < PLAN_NT; off <<= 1) {  // inclusive Hillis-Steele scan
-    int vu = 0, vs = 0, vk = 0;
-    if (tid >= off) {
-      vu = scan_u[tid - off];
-      vs = scan_s[tid - off];
-      vk = scan_k[tid - off];
+  // Inclusive scans over the threads: within each wave by shuffles, then across the
+  // waves' totals.
+  int iu = my_u, is = my_s, ik = my_k;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int ou = __shfl_up(iu, off), os = __shfl_up(is, off), ok = __shfl_up(ik, off);
+    if (lane >= off) {
+      iu += ou;
+      is += os;
+      ik += ok;
     }
-    __syncthreads();
-    scan_u[tid] += vu;
-    scan_s[tid] += vs;
-    scan_k[tid] += vk;
-    __syncthreads();
   }
-  const int U = scan_u[PLAN_NT - 1];
-  int ub = scan_u[tid] - my_u, sb = scan_s[tid] - my_s, kb = scan_k[tid] - my_k;
+  if (lane == 63) {
+    s_wsum[0][wave] = iu;
+    s_wsum[1][wave] = is;
+    s_wsum[2][wave] = ik;
+  }
+  __syncthreads();
+  int U = 0, NS = 0, NK = 0, pu = 0, ps = 0, pk = 0;
+#pragma unroll
+  for (int i = 0; i < PLAN_WAVES; ++i) {
+    if (i < wave) {
+      pu += s_wsum[0][i];
+      ps += s_wsum[1][i];
+      pk += s_wsum[2][i];
+    }
+    U += s_wsum[0][i];
+    NS += s_wsum[1][i];
+    NK += s_wsum[2][i];
+  }
+  int ub = pu + iu - my_u, sb = ps + is - my_s, kb = pk + ik - my_k;
   const bool decode_like = (long long)a.T <= 4 * (long long)a.B;
   // runs: every unit starts at once and some token is split (its units share Q rows)
   const bool runs = U <= a.target && U > a.T;
   for (int t = t0; t < t1; ++t) {
     int* r = tok + (size_t)t * SAS_TOK_W;
-    const int b = r[TK_B];
-    const long long rows = b >= 0 ? (long long)r[TK_NWIN] + r[TK_NCMPMAX] : 0;
+    const int rv = tok_rows(t);
+    const long long rows = max(rv, 0);
     const int splits = rows > chunk ? (int)((rows + chunk - 1) / chunk) : 1;
-    r[TK_SPLITS] = splits;
-    r[TK_WSBASE] = splits > 1 ? sb : -1;
+    *reinterpret_cast<int2*>(r + TK_SPLITS) = make_int2(splits, splits > 1 ? sb : -1);
     long long ct = rows;
     if (splits > 1) ct = ((rows + splits - 1) / splits + SAS_TILE - 1) / SAS_TILE * SAS_TILE;
     for (int i = 0; i < splits; ++i) {
@@ -228,12 +274,9 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
       const int k = U - 1 - (ub + i);
       const int slot = !decode_like ? k : runs ? xcd_run_slot(k, U) : xcd_pair_slot(k, U);
       if (slot < 0 || slot >= L.unit_cap) continue;  // (U <= unit_cap: flagged below if not)
-      int* ur = units + (size_t)slot * SAS_UNIT_W;
       long long r0 = (long long)i * ct, r1 = r0 + ct < rows ? r0 + ct : rows;
-      ur[0] = t;
-      ur[1] = (int)r0;
-      ur[2] = (int)r1;
-      ur[3] = b >= 0 ? i : -1;
+      *reinterpret_cast<int4*>(units + (size_t)slot * SAS_UNIT_W) =
+          make_int4(t, (int)r0, (int)r1, rv >= 0 ? i : -1);
     }
     ub += splits;
     if (splits > 1) {
@@ -253,8 +296,8 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     plan[PH_UNITS] = U;
     plan[PH_CHUNK] = (int)chunk;
     plan[PH_TARGET] = a.target;
-    plan[PH_NSPLIT_TOKENS] = scan_k[PLAN_NT - 1];
-    plan[PH_NSLOTS] = scan_s[PLAN_NT - 1];
+    plan[PH_NSPLIT_TOKENS] = NK;
+    plan[PH_NSLOTS] = NS;
     plan[PH_TOTAL_ROWS_LO] = (int)(R & 0xffffffff);
     plan[PH_TOTAL_ROWS_HI] = (int)(R >> 32);
     plan[PH_H] = a.H;
@@ -270,8 +313,8 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     // that broke one is refused by every kernel.
     int status = 0;
     if ((long long)U > L.unit_cap) status |= PS_UNITS_OVER_CAP;
-    if ((long long)scan_s[PLAN_NT - 1] > 2 * (long long)a.target) status |= PS_SLOTS_OVER_CAP;
-    if ((long long)scan_k[PLAN_NT - 1] > L.split_cap) status |= PS_SPLIT_TOKENS_OVER_CAP;
+    if ((long long)NS > 2 * (long long)a.target) status |= PS_SLOTS_OVER_CAP;
+    if ((long long)NK > L.split_cap) status |= PS_SPLIT_TOKENS_OVER_CAP;
     plan[PH_STATUS] = status;
     for (int i = PH_STATUS + 1; i < SAS_PLAN_HDR; ++i) plan[i] = 0;
   }

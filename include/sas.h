@@ -122,7 +122,8 @@ int sas_target_units(const sas_params_t* p, int32_t* units);
 
 /* ---- device entry points (asynchronous on stream) ---- */
 /* Split-KV scheduler: per-token row spans and work units balanced over CUs,
- * from q_prefix / act_q_lens / seqused_kv only (device pointers). */
+ * from q_prefix / act_q_lens / seqused_kv only (device pointers).  plan must be
+ * 16-byte aligned (SAS_ERR_SHAPE otherwise). */
 int sas_plan(const sas_params_t* p, const int32_t* q_prefix, const int32_t* act_q_lens,
              const int32_t* seqused_kv, int32_t* plan, size_t plan_n_int32, sas_stream_t stream);
 /* Full forward: (plan if plan == NULL) -> index resolution -> attention ->
