@@ -192,13 +192,16 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
   // first, which doubles the time of the CUs that run one, and it splits more
   // tokens (each split unit writes a partial the combine pass reads back).
   if (a.T < a.target) {
-    auto units_at = [&](long long c) {
-      long long n = 0;
+    // (32-bit arithmetic: a token's rows and the chunk fit, and the GPU has no 64-bit
+    // integer divide)
+    auto units_at = [&](long long c64) {
+      const unsigned c = (unsigned)c64;
+      int n = 0;
       for (int t = t0; t < t1; ++t) {
-        const long long rows = max(tok_rows(t), 0);
-        n += rows > c ? (rows + c - 1) / c : 1;
+        const unsigned rows = (unsigned)max(tok_rows(t), 0);
+        n += rows > c ? (int)((rows + c - 1) / c) : 1;
       }
-      return n;
+      return (long long)n;
     };
     const long long longest = block_reduce(my_longest, true);
     long long lo = chunk;  // [lo, hi]: multiples of the tile; hi gives one unit per token
@@ -213,10 +216,17 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     chunk = lo;
   }
 
+  // a token's split count (32-bit division when the chunk fits, as it always does in
+  // practice: a token's rows fit an int)
+  auto splits_of = [&](long long rows) -> int {
+    if (rows <= chunk) return 1;
+    if (chunk <= 0x7fffffffll) return (int)(((unsigned)rows + (unsigned)chunk - 1u) / (unsigned)chunk);
+    return (int)((rows + chunk - 1) / chunk);
+  };
   int my_u = 0, my_s = 0, my_k = 0;
   for (int t = t0; t < t1; ++t) {
     const long long rows = max(tok_rows(t), 0);
-    int splits = rows > chunk ? (int)((rows + chunk - 1) / chunk) : 1;
+    int splits = splits_of(rows);
     my_u += splits;
     if (splits > 1) {
       my_s += splits;
@@ -261,7 +271,7 @@ __global__ __launch_bounds__(PLAN_NT) void plan_kernel(SasPlanArgs a,
     int* r = tok + (size_t)t * SAS_TOK_W;
     const int rv = tok_rows(t);
     const long long rows = max(rv, 0);
-    const int splits = rows > chunk ? (int)((rows + chunk - 1) / chunk) : 1;
+    const int splits = splits_of(rows);
     *reinterpret_cast<int2*>(r + TK_SPLITS) = make_int2(splits, splits > 1 ? sb : -1);
     long long ct = rows;
     if (splits > 1) ct = ((rows + splits - 1) / splits + SAS_TILE - 1) / SAS_TILE * SAS_TILE;
