@@ -184,12 +184,32 @@ int launch_attend(const sas_params_t* p, const sas_tensors_t* t, const int32_t* 
   const SasFwdArgs a = fwd_args(p, target);
   sas::SasResolveArgs r = resolve_args(p, t, w);
   if (!resolve) r.addr = nullptr;
+  r.rows = nullptr;  // the forward needs addresses only (sas_resolve also writes the codes)
   hipExtLaunchKernelGGL(pick_attend(p), dim3(a.unit_cap), dim3(256), 0, (hipStream_t)stream,
                         (hipEvent_t)start_event, (hipEvent_t)stop_event, 0, a,
                         static_cast<const uint16_t*>(t->q), static_cast<const uint64_t*>(w.addr),
                         static_cast<const float*>(w.scale), static_cast<const int*>(w.ncmp),
                         t->sinks, static_cast<const int*>(plan), static_cast<uint16_t*>(t->out),
                         t->lse, w.o, w.ml, r);
+  return launch_status();
+}
+
+// The resolver stage; codes: also write the row codes (the forward reads addresses
+// only; the backward and sas_debug_rows read the codes).
+int resolve_stage(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
+                  size_t ws_bytes, sas_stream_t stream, bool codes) {
+  int rc = sas_validate(p);
+  if (rc) return rc;
+  if ((rc = check_tensors(p, t))) return rc;
+  const int target = target_units(p);
+  Ws w;
+  if ((rc = carve(p, ws, ws_bytes, target, &w))) return rc;
+  if (!plan) plan = w.plan;
+  if (p->total_tokens == 0) return SAS_OK;
+  sas::SasResolveArgs r = resolve_args(p, t, w);
+  if (!codes) r.rows = nullptr;
+  hipLaunchKernelGGL(sas::resolve_kernel, dim3(p->total_tokens), dim3(sas::RS_NT), 0,
+                     (hipStream_t)stream, fwd_args(p, target), plan, r);
   return launch_status();
 }
 
@@ -299,17 +319,7 @@ int sas_plan(const sas_params_t* p, const int32_t* q_prefix, const int32_t* act_
 
 int sas_resolve(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
                 size_t ws_bytes, sas_stream_t stream) {
-  int rc = sas_validate(p);
-  if (rc) return rc;
-  if ((rc = check_tensors(p, t))) return rc;
-  const int target = target_units(p);
-  Ws w;
-  if ((rc = carve(p, ws, ws_bytes, target, &w))) return rc;
-  if (!plan) plan = w.plan;
-  if (p->total_tokens == 0) return SAS_OK;
-  hipLaunchKernelGGL(sas::resolve_kernel, dim3(p->total_tokens), dim3(sas::RS_NT), 0,
-                     (hipStream_t)stream, fwd_args(p, target), plan, resolve_args(p, t, w));
-  return launch_status();
+  return resolve_stage(p, t, plan, ws, ws_bytes, stream, true);
 }
 
 int sas_attend_timed(const sas_params_t* p, const sas_tensors_t* t, const int32_t* plan, void* ws,
@@ -377,7 +387,7 @@ int sas_forward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* pl
   if ((int64_t)p->total_tokens <= (int64_t)target) {
     if ((rc = launch_attend(p, t, plan, w, target, stream, nullptr, nullptr, true))) return rc;
   } else {
-    if ((rc = sas_resolve(p, t, plan, ws, ws_bytes, stream))) return rc;
+    if ((rc = resolve_stage(p, t, plan, ws, ws_bytes, stream, false))) return rc;
     if ((rc = sas_attend(p, t, plan, ws, ws_bytes, stream))) return rc;
   }
   return sas_combine(p, t, plan, ws, ws_bytes, stream);

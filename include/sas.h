@@ -191,7 +191,8 @@ int sas_backward(const sas_params_t* p, const sas_tensors_t* t, const int32_t* p
 /* Debug: copy the resolved row-code lists of every token into rows (int32
  * [T, win_left + 1 (+ topk in scenarios 2, 3)]: the token's window pool rows, then
  * directly after them its compressed pool rows; -1 = a row read as zeros) and the
- * compressed-row counts into counts [T]. */
+ * compressed-row counts into counts [T].  The codes are those of the last
+ * sas_resolve on this workspace (sas_forward writes pool addresses only). */
 int sas_debug_rows(const sas_params_t* p, const void* workspace, int32_t* rows, int32_t* counts,
                    sas_stream_t stream);
 

@@ -294,7 +294,10 @@ def test_resolution_bit_exact(kind):
         act_q_lens=d["cu_seqlens_q"][1:] - d["cu_seqlens_q"][:-1], seqused_kv=d["seqused_kv"],
         sinks=d["sinks"], metadata=None, scenario=3, topk=c.K, cmp_ratio=4, ori_win_left=127,
         softmax_scale=c.softmax_scale, core_num=256)
+    # the forward plans into the workspace; the resolver stage then writes the row
+    # codes (the forward writes addresses only)
     launch.run()
+    launch.run("resolve")
     W = 128
     rows = torch.zeros((c.T, W + c.K), dtype=torch.int32, device="cuda")  # list capacity
     cnt = torch.zeros(c.T, dtype=torch.int32, device="cuda")
