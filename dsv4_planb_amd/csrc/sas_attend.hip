@@ -1169,7 +1169,8 @@ __device__ __forceinline__ bool attend_unit(
 namespace sas {
 
 // One workgroup per work unit.  rs.addr set: the resolver stage did not run, and
-// each unit first resolves its own rows (lists, scales, codes) into the workspace.
+// each unit first resolves its own rows (pool addresses, fp8 scales and the
+// compressed-row count; rs.rows is null, so no row codes) into the workspace.
 template <int DQK, int QT, bool STREAM, bool KV8>
 __global__ __launch_bounds__(256, 1) void attend_kernel(
     SasFwdArgs a, const uint16_t* __restrict__ q, const uint64_t* addr_list,

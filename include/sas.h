@@ -129,8 +129,9 @@ int sas_plan(const sas_params_t* p, const int32_t* q_prefix, const int32_t* act_
 /* Full forward: (plan if plan == NULL) -> index resolution -> attention ->
  * split combine.  With at most as many tokens as balance-target units, every
  * work unit resolves its own rows at the start of the attention kernel instead
- * of a resolution stage of its own (same lists, codes and counts in the
- * workspace).  plan may be a buffer filled by sas_plan for the same params
+ * of a resolution stage of its own (same address and scale lists and counts in
+ * the workspace; the forward writes no row codes, which sas_resolve adds).
+ * plan may be a buffer filled by sas_plan for the same params
  * and lengths.  The plan's header records the arguments it was built for (token
  * and batch counts, scenario, window, ratio, top-k, balance target); the kernels
  * refuse a plan whose record differs from the call: the outputs are written as
