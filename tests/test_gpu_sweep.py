@@ -1,0 +1,79 @@
+"""GPU parity over seeded random configurations.
+
+Each seed draws one call from the whole validated parameter space: head count
+(1..128), scenario (1, 2, 3), top-k, compression ratio, page sizes, window
+length, per-sequence query counts, ragged KV lengths, query dtype (bf16 /
+fp16), KV dtype (16-bit / fp8 e4m3) and d_qk (512 / 576).  Every draw is
+checked against the oracle and the float64 exact value with the same rules as
+the fixed cases (tests/gpu_helpers.py).  The draws are deterministic, so a
+failure names a reproducible configuration; ``sweep_config`` is also run on
+the CPU (without the device) to keep every draw valid and the oracle quick.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.cases import make_case
+from tests.gpu_helpers import assert_parity, run_op
+
+SEEDS = list(range(24))
+
+
+def sweep_config(seed: int) -> dict:
+    """The make_case arguments of sweep draw ``seed``."""
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 7))
+    scenario = int(rng.choice([1, 2, 3], p=[0.2, 0.2, 0.6]))
+    q_dtype = str(rng.choice(["bf16", "fp16"]))
+    kv_dtype = "fp8e4m3" if rng.random() < 0.35 else q_dtype
+    q_per = [int(v) for v in rng.integers(1, 5, size=B)]
+    seq_kv = np.exp(rng.uniform(0.0, np.log(50000.0), size=B)).astype(int) + 1
+    cfg = dict(
+        B=B,
+        H=int(rng.choice([1, 5, 16, 33, 64, 100, 128])),
+        seq_kv=[max(int(v), q) for v, q in zip(seq_kv, q_per)],  # a sequence holds its queries
+        q_per_seq=q_per,
+        scenario=scenario,
+        K=int(rng.choice([1, 7, 64, 300, 512, 2048])),
+        D=int(rng.choice([512, 576])),
+        cmp_ratio=int(rng.choice([1, 2, 4, 16, 128])),
+        block_size=int(rng.choice([16, 64, 128])),
+        cmp_block_size=int(rng.choice([16, 64])),
+        win_left=int(rng.choice([0, 3, 31, 127, 200])),
+        q_dtype=q_dtype,
+        kv_dtype=kv_dtype,
+        seed=seed,
+    )
+    return cfg
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_sweep_config_is_valid(seed):
+    """Every draw stays inside what the C ABI's argument guards (sas_validate)
+    accept: head count, scenario, dtypes, dimensions, top-k and ratio; every
+    sequence holds its queries, and the case builds with the drawn token count."""
+    cfg = sweep_config(seed)
+    assert 1 <= cfg["H"] <= 128 and cfg["scenario"] in (1, 2, 3)
+    assert cfg["kv_dtype"] in (cfg["q_dtype"], "fp8e4m3")
+    assert cfg["D"] in (512, 576) and cfg["K"] >= 1 and cfg["cmp_ratio"] >= 1
+    assert all(q <= kv for q, kv in zip(cfg["q_per_seq"], cfg["seq_kv"]))
+    c = make_case(**cfg)
+    assert c.T == sum(cfg["q_per_seq"])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", SEEDS)
+def test_sweep_parity(seed):
+    cfg = sweep_config(seed)
+    c = make_case(**cfg)
+    print(f"\n[case] sweep{seed}: B={c.B} T={c.T} H={c.H} D={c.D} scen={c.scenario} K={c.K} "
+          f"ratio={cfg['cmp_ratio']} win={cfg['win_left']} pages={cfg['block_size']}/"
+          f"{cfg['cmp_block_size']} kv={c.kv_dtype} q={c.q_dtype} seq_kv={cfg['seq_kv']} "
+          f"q_per={cfg['q_per_seq']}", flush=True)
+    out, lse = run_op(c)
+    ref, ref_lse = c.oracle_c()
+    ex, ex_lse = c.oracle_exact()
+    assert_parity(out, lse, ref, ref_lse, dtype=c.q_dtype, label=f"sweep{seed}",
+                  exact=(ex, ex_lse), kv8=c.kv_dtype == "fp8e4m3")
