@@ -27,7 +27,11 @@ give the per-call distribution.  ``roofline`` rates the attention kernel alone:
 ``--steps`` back-to-back launches on its stream, each dispatch recording its own
 start and end into HIP events (``sas_attend_timed``), so ``kernel_us`` is the
 kernel's execution time as a kernel trace reports it; ``attend_us`` is the same
-launches timed by events around them, dispatch gaps included.
+launches timed by events around them, dispatch gaps included.  After everything
+else, the headline workload runs ``--sustain`` seconds (default 5) of
+back-to-back replays and times ``--steps`` replays again, reported as
+``sustained``: under the socket's power limit the clock keeps falling over
+seconds of load.
 ``cpu_baseline`` times the C oracle on a bounded sample of the same workload on
 the host cores and scales it to the full call.
 """
@@ -251,7 +255,7 @@ def _settle(fn, secs, stream):
     return n
 
 
-def measure(wl, steps, warmup, core_num=256, settle_s=0.25):
+def measure(wl, steps, warmup, core_num=256, settle_s=0.25, sustain_s=0.0):
     """Per workload: build the plan and launch, capture the forward call in a
     hipGraph, then (1) the first 20 replays timed one by one from a cold start
     (`cold_call_us`: the clock transient), (2) a settle phase of `settle_s`
@@ -262,7 +266,10 @@ def measure(wl, steps, warmup, core_num=256, settle_s=0.25):
     by their own dispatch events (`attend_kernel_us`, the roofline's kernel time)
     and by events around them (`attend_us`), (7) the other stages, the forward
     call launched eagerly through the C ABI (`eager_call_us`) and the eager API
-    call."""
+    call, (8) with `sustain_s` > 0, last (so that no figure above moves): that
+    many seconds of back-to-back replays, then `steps` replays timed again
+    (`sustained`).  The socket's power limit keeps lowering the clock over
+    seconds of load, so this reads above `call_us`."""
     from dsv4_planb_amd import sparse_attn_sharedkv
     from dsv4_planb_amd.graph import SasGraph
 
@@ -322,6 +329,11 @@ def measure(wl, steps, warmup, core_num=256, settle_s=0.25):
             sparse_attn_sharedkv(wl["q"], **api_kw)
         torch.cuda.synchronize()
         eager_us = (time.perf_counter() - t1) * 1e6 / steps
+        sustained = None
+        if sustain_s > 0:
+            n_sus = _settle(replay, sustain_s, stream)
+            sustained = {"seconds": sustain_s, "calls": n_sus,
+                         "call_us": _events_time(replay, steps, stream)}
         graph.close()
     ok = bool(torch.isfinite(out.float()).all().item())
     return dict(call_us=call_us, eager_call_us=eager_call_us, attend_us=attend_us,
@@ -330,7 +342,7 @@ def measure(wl, steps, warmup, core_num=256, settle_s=0.25):
                 eager_api_us=eager_us, finite=ok, call_dist_us=call_dist,
                 attend_dist_us=attend_dist, cold_call_us=[round(x, 1) for x in cold],
                 settle={"seconds": settle_s, "calls": settle_calls,
-                        "attend_calls": attend_settle})
+                        "attend_calls": attend_settle}, sustained=sustained)
 
 
 def _traffic_from_profile(workload):
@@ -603,6 +615,10 @@ def main():
                              "mfma_probe", "read_probe"],
                     help="what --mode power runs")
     ap.add_argument("--secs", type=float, default=10.0, help="--mode power duration")
+    ap.add_argument("--sustain", type=float, default=5.0,
+                    help="seconds of back-to-back replays after every other timing of the headline "
+                         "workload, then `steps` replays timed again (reported as 'sustained'; "
+                         "0 skips it)")
     ap.add_argument("--compact", action="store_true",
                     help="--mode power / attend / forward: all sequences read the first "
                          "sequence's KV pages")
@@ -636,7 +652,8 @@ def main():
         _log(f"{name}: building inputs")
         wl = make_workload(name, seed=0, dev=dev)
         _log(f"{name}: timing")
-        r = measure(wl, args.steps, args.warmup, settle_s=args.settle)
+        r = measure(wl, args.steps, args.warmup, settle_s=args.settle,
+                    sustain_s=args.sustain if name == args.workload else 0.0)
         _log(f"{name}: call {r['call_us']:.1f} us, attend {r['attend_us']:.1f} us "
              f"(kernel {r['attend_kernel_us']:.1f} us)")
         attend_s = r["attend_kernel_us"] * 1e-6  # the kernel's own dispatch time
